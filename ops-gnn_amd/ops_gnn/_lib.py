@@ -1,0 +1,108 @@
+"""Loader for libogn_hip.so, the gfx950 kernels behind the C ABI in include/ogn.h.
+
+Replaces the reference's npu-smi / CANN_TARGET target selection
+(reference python/ops_gnn/_device.py:15-44, python/ops_gnn/__init__.py:27-42):
+there is exactly one build, for gfx950, living next to this file.  A missing
+or unloadable library raises ImportError -- there is no CPU fallback.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime first so the library shares it)
+
+LIB_NAME = "libogn_hip.so"
+LIB_PATH = Path(os.environ.get("OGN_LIB", Path(__file__).resolve().parent / LIB_NAME))
+
+try:
+    _so = ctypes.CDLL(str(LIB_PATH))
+except OSError as exc:  # pragma: no cover - exercised only on a broken install
+    raise ImportError(
+        f"ops_gnn: cannot load the gfx950 kernel library {LIB_PATH} ({exc}). "
+        "Build it with `python ops-gnn_amd/build.py` (or __graft_entry__.build())."
+    ) from exc
+
+arch = "gfx950"
+
+# dtype codes (include/ogn.h ogn_dtype)
+F32, F16, BF16, I8, I32, I64, F64, U8 = range(8)
+TORCH_TO_OGN = {
+    torch.float32: F32,
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.int8: I8,
+    torch.int32: I32,
+    torch.int64: I64,
+    torch.float64: F64,
+    torch.uint8: U8,
+}
+
+OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); every entry must be declared in include/ogn.h.
+SIGNATURES = {
+    "ogn_last_error": (ctypes.c_char_p, []),
+    "ogn_arch": (ctypes.c_char_p, []),
+    "ogn_abi_version": (_int, []),
+    "ogn_timing_enable": (_int, [_int]),
+    "ogn_timing_query": (_int, [ctypes.c_char_p, _vp, _vp]),
+    "ogn_validate_csr": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
+    "ogn_spmm_csr_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _int, _int]),
+    "ogn_spmm_csr": (_int, [_vp, _vp, _int, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _i64,
+                            _vp, _int, _vp, _int, _vp, _sz, _vp]),
+    "ogn_ind2ptr": (_int, [_vp, _int, _i64, _i64, _vp, _vp]),
+    "ogn_ptr2ind": (_int, [_vp, _int, _i64, _i64, _vp, _vp]),
+}
+
+for _name, (_res, _args) in SIGNATURES.items():
+    _fn = getattr(_so, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+lib = _so
+
+
+def check(rc: int, what: str) -> None:
+    """Turn a C-ABI status into the exception the reference raises (RuntimeError,
+    like its TORCH_CHECK failures)."""
+    if rc != OK:
+        msg = _so.ogn_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {msg or 'error code %d' % rc}")
+
+
+def dptr(t):
+    """Device address of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    """hipStream_t of torch's current stream on the tensor's device."""
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_gpu(*tensors, what="ops_gnn"):
+    for t in tensors:
+        if t is not None and (not isinstance(t, torch.Tensor) or t.device.type != "cuda"):
+            raise ValueError(f"{what}: tensors must be on the GPU (torch 'cuda' device on ROCm)")
+
+
+def workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def timing_enable(on: bool) -> None:
+    check(_so.ogn_timing_enable(1 if on else 0), "timing_enable")
+
+
+def timing_query(kernel: str):
+    """(total_ms, launches) of the recorded launches of `kernel`."""
+    total = ctypes.c_double(0.0)
+    count = ctypes.c_int64(0)
+    check(_so.ogn_timing_query(kernel.encode(), ctypes.byref(total), ctypes.byref(count)), "timing_query")
+    return total.value, count.value

@@ -1,0 +1,145 @@
+"""Python face of the CPU oracle (oracle.c) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, as the checker and the timed CPU baseline.  The product package
+(ops_gnn) never imports it.
+
+Functions take numpy arrays (or CPU torch tensors), widen floating inputs to
+float32 (exact for fp16/bf16), and return float64 values (+ int64 arg) so the
+caller can apply the reference golden's final cast.
+"""
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "liboracle.so"
+
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_lib = None
+
+REDUCE = {"sum": 0, "add": 0, "mean": 1, "min": 2, "max": 3}
+
+
+def build() -> Path:
+    """Compile oracle.c with the committed Makefile (gcc + OpenMP)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        l = ctypes.CDLL(str(LIB_PATH))
+        vp = ctypes.c_void_p
+        i64 = ctypes.c_int64
+        l.oracle_spmm_csr.argtypes = [_i64p, _i64p, vp, i64, _f32p, i64, i64, i64, i64,
+                                      ctypes.c_int, _f64p, vp]
+        l.oracle_spmm_csr.restype = None
+        l.oracle_ind2ptr.argtypes = [_i64p, i64, i64, _i64p]
+        l.oracle_ptr2ind.argtypes = [_i64p, i64, i64, _i64p]
+        l.oracle_segment_csr.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, ctypes.c_int,
+                                         _f64p, vp]
+        _lib = l
+    return _lib
+
+
+def _np(x, dtype=None):
+    if hasattr(x, "detach"):  # torch tensor
+        x = x.detach().cpu()
+        if dtype is not None and x.is_floating_point():
+            x = x.float()
+        x = x.numpy()
+    x = np.asarray(x)
+    if dtype is not None:
+        x = x.astype(dtype, copy=False)
+    return np.ascontiguousarray(x)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def spmm_csr(ptr, col, value, mat, reduce="sum"):
+    """torch_sparse SpMM golden (reference test/torch_sparse_spmm/arch35/golden.py:91-116).
+
+    mat: [..., N, K]; value: None, [E] or [E, K].  Returns (out float64
+    [..., M, K], arg int64 [..., M, K] or None for sum/mean).
+    """
+    ptr = _np(ptr, np.int64)
+    col = _np(col, np.int64)
+    mat = _np(mat, np.float32)
+    lead = mat.shape[:-2]
+    n, k = mat.shape[-2], mat.shape[-1]
+    batch = int(np.prod(lead)) if lead else 1
+    m = ptr.shape[0] - 1
+    width = 0
+    v = None
+    if value is not None:
+        v = _np(value, np.float32).reshape(col.shape[0], -1)
+        width = v.shape[1]
+        if width not in (1, k):
+            raise ValueError("value width must be 1 or K")
+        v = np.ascontiguousarray(v)
+    r = REDUCE[reduce]
+    out = np.zeros(lead + (m, k), dtype=np.float64)
+    arg = np.zeros(lead + (m, k), dtype=np.int64) if r >= 2 else None
+    lib().oracle_spmm_csr(ptr, col, _ptr(v), width, mat, batch, m, n, k, r, out, _ptr(arg))
+    return out, arg
+
+
+def ind2ptr(ind, rows):
+    """reference test/sparse/arch35/golden.py:6-27."""
+    ind = _np(ind, np.int64)
+    out = np.zeros(rows + 1, dtype=np.int64)
+    lib().oracle_ind2ptr(ind, ind.shape[0], rows, out)
+    return out
+
+
+def ptr2ind(ptr, numel):
+    """reference test/sparse/arch35/golden.py:30-43."""
+    ptr = _np(ptr, np.int64)
+    out = np.zeros(numel, dtype=np.int64)
+    lib().oracle_ptr2ind(ptr, ptr.shape[0] - 1, numel, out)
+    return out
+
+
+def segment_csr(src, indptr, reduce="sum"):
+    """segment_csr golden (reference test/segment_csr/arch35/golden.py:21-103).
+
+    Returns (values float64, arg int64 or None).  Reduction axis is
+    indptr.dim() - 1; leading indptr dims broadcast to src's.
+    """
+    src = _np(src, np.float32)
+    ip = _np(indptr, np.int64)
+    dim = ip.ndim - 1
+    lead = src.shape[:dim]
+    length = src.shape[dim]
+    feat = int(np.prod(src.shape[dim + 1:])) if src.ndim > dim + 1 else 1
+    batch = int(np.prod(lead)) if lead else 1
+    segs = ip.shape[-1] - 1
+    if ip.ndim > 1 and int(np.prod(ip.shape[:-1])) != 1:
+        ip = np.ascontiguousarray(np.broadcast_to(ip, lead + (ip.shape[-1],)))
+        stride = ip.shape[-1]
+    else:
+        ip = np.ascontiguousarray(ip.reshape(-1))
+        stride = 0
+    r = REDUCE[reduce]
+    shape = lead + (segs,) + src.shape[dim + 1:]
+    out = np.zeros(shape, dtype=np.float64)
+    arg = np.zeros(shape, dtype=np.int64) if r >= 2 else None
+    lib().oracle_segment_csr(np.ascontiguousarray(src.reshape(-1)), ip.reshape(-1), stride, batch,
+                             length, feat, segs, r, out, _ptr(arg))
+    return out, arg
+
+
+def threads() -> int:
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))

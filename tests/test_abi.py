@@ -1,0 +1,57 @@
+"""C-ABI surface checks (CPU only: load + symbol table, no kernel launches)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ogn.h"
+LIB = ROOT / "ops-gnn_amd" / "ops_gnn" / "libogn_hip.so"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(ogn_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_functions():
+    names = declared_functions()
+    assert "ogn_spmm_csr" in names and "ogn_last_error" in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(LIB))
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared in ogn.h but not exported: {missing}"
+
+
+def test_python_bindings_cover_header_exactly():
+    import ops_gnn._lib as L
+
+    assert sorted(L.SIGNATURES) == declared_functions()
+
+
+def test_identification_calls():
+    import ops_gnn._lib as L
+
+    assert L.lib.ogn_arch() == b"gfx950"
+    assert L.lib.ogn_abi_version() >= 1
+    assert L.lib.ogn_last_error() == b""
+
+
+def test_argument_errors_are_reported_without_gpu():
+    import ops_gnn._lib as L
+
+    rc = L.lib.ogn_spmm_csr(None, None, 7, None, 1, None, 0, 1, 1, 1, 1, 0, None, 0, None, 0, None, 0, None)
+    assert rc == L.EINVAL
+    assert b"index dtype" in L.lib.ogn_last_error()
+    rc = L.lib.ogn_ind2ptr(None, L.I64, -1, 3, None, None)
+    assert rc == L.EINVAL and b"negative" in L.lib.ogn_last_error()
+
+
+def test_workspace_query_is_pure_host():
+    import ops_gnn._lib as L
+
+    a = L.lib.ogn_spmm_csr_workspace_size(100, 1000, 128, 1, L.F32, 0)
+    b = L.lib.ogn_spmm_csr_workspace_size(100, 1000, 128, 1, L.F32, 3)
+    assert 0 < a < b
