@@ -87,6 +87,8 @@ def main():
     ap.add_argument("--reduce", choices=["sum", "max", "min"], default="sum")
     ap.add_argument("--scale", type=float, default=1.0, help="fraction of the config-3 size (testing)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (rocprof counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -146,6 +148,14 @@ def main():
         rows_ms, _ = _lib.timing_query("spmm_chunk_rows")
         fix_ms, _ = _lib.timing_query("spmm_fixup")
         _lib.timing_enable(False)
+
+        if args.copy_calibration:
+            src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
 
     esz = 4 if args.dtype == "f32" else 2
     mm = args.reduce in ("min", "max")
