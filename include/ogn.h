@@ -51,7 +51,9 @@ typedef enum {
   OGN_REDUCE_SUM = 0,
   OGN_REDUCE_MEAN = 1,
   OGN_REDUCE_MIN = 2,
-  OGN_REDUCE_MAX = 3
+  OGN_REDUCE_MAX = 3,
+  OGN_REDUCE_PROD = 4, /* scatter "mul" */
+  OGN_REDUCE_LSE = 5   /* log-sum-exp */
 } ogn_reduce;
 
 enum {
@@ -130,6 +132,113 @@ int ogn_ind2ptr(const void* ind, int index_dtype, int64_t numel, int64_t rows, i
  */
 int ogn_ptr2ind(const void* ptr, int index_dtype, int64_t rows, int64_t numel, int64_t* out,
                 void* stream);
+
+/* ------------------------------------------------------------------ segment reductions
+ * Reductions over runs of consecutive rows.  src is viewed as
+ * [batch, length, k] (batch = product of the dims before the reduction dim,
+ * k = product of the dims after it); out / arg as [batch, segments, k].
+ * indptr: int64 [ptr_batches, segments + 1], ptr_batches 1 (shared by every
+ * batch) or `batch`; non-decreasing, within [0, length].  Segment s covers
+ * rows [indptr[s], indptr[s+1]); rows outside [indptr[0], indptr[segments])
+ * are ignored.  dtype: f32 / f16 / bf16 for src and out; arithmetic in fp32.
+ * reduce: sum, mean, min, max, prod, lse.  arg (int64, optional, min/max
+ * only) gets positions along the reduction dim.
+ *
+ * semantics selects the reference operator whose rules apply:
+ *  OGN_SEM_SEGMENT_CSR -- segment_csr (reference test/segment_csr/arch35/golden.py:21-103,
+ *    csrc/npu/segment_csr/op_kernel/arch35/segment_csr.cpp:506-640): out is
+ *    overwritten; min/max start from +-inf and move on strict improvement
+ *    (first extremum wins, NaN never enters, an all-NaN segment gives +-inf
+ *    with arg = its first row); empty segments give 0 / arg = length.
+ *  OGN_SEM_SEGMENT_COO -- Ascend 950 segment_coo (reference
+ *    csrc/npu/segment_coo/op_kernel/arch35/segment_coo.cpp:114-153): sum
+ *    overwrites; mean adds to out when OGN_SEG_HAS_OUT; min/max fold with
+ *    <= / >= from the seed (out with arg = length if OGN_SEG_HAS_OUT, else
+ *    the segment's first row), so the LAST extremum wins.
+ *  OGN_SEM_SCATTER -- torch_scatter scatter on a sorted index (reference
+ *    test/scatter/arch35/golden.py:35-127): sum/mean/prod accumulate into out
+ *    when OGN_SEG_HAS_OUT (else start from 0 / 1); mean divides by the count
+ *    (empty: out unchanged); min/max fold with <= / >= from out (or from the
+ *    dtype's finite extreme, a position never written giving 0), last
+ *    extremum wins, arg = length when nothing was taken.
+ *  reduce = lse gives log(sum(exp(x))) with the shift clamped to +-FLT_MAX
+ *    (reference csrc/npu/segment_logsumexp/op_kernel/common/segment_logsumexp_kernel.h:10-45);
+ *    empty segments give -inf.
+ * Replaces the segment_csr / segment_coo / segment_logsumexp host+kernel
+ * pairs (reference csrc/npu/segment_csr/op_host/segment_csr.cpp:1663-1702,
+ * csrc/npu/segment_coo/op_host/segment_coo.cpp:1127-1175).
+ */
+enum { OGN_SEM_SEGMENT_CSR = 0, OGN_SEM_SEGMENT_COO = 1, OGN_SEM_SCATTER = 2 };
+enum { OGN_SEG_HAS_OUT = 1 };
+size_t ogn_segment_reduce_workspace_size(int64_t batch, int64_t length, int64_t segments, int64_t k,
+                                         int64_t ptr_batches, int dtype, int reduce);
+int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* src, int dtype,
+                       int64_t batch, int64_t length, int64_t segments, int64_t k, void* out,
+                       int64_t* arg, int reduce, int semantics, int flags, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* Batched ind2ptr over int64 sorted indices: ind [batches, numel] ->
+ * out [batches, rows + 1].  Used to turn a sorted COO index into segment
+ * pointers (reference segment_coo BuildPointers,
+ * csrc/npu/segment_coo/op_kernel/arch35/segment_coo.cpp:67-82). */
+int ogn_ind2ptr_batched(const int64_t* ind, int64_t batches, int64_t numel, int64_t rows, int64_t* out,
+                        void* stream);
+
+/* Facts about an int64 index (device memory, 3 x int64): facts[0] = 1 if
+ * not non-decreasing, facts[1] = min, facts[2] = max (INT64_MAX / INT64_MIN
+ * when empty).  Replaces the cached index min/max probe of the reference
+ * scatter (python/ops_gnn/scatter.py:134-178). */
+int ogn_index_facts(const int64_t* ind, int64_t numel, int64_t* facts, void* stream);
+
+/* Log-sum-exp statistics of sorted groups (contiguous segments, shared
+ * indptr [segments + 1]): m_out[b, g, f] = max (unclamped; -inf for an empty
+ * group) and s_out[b, g, f] = sum(exp(x - clamp(max, +-FLT_MAX))), both fp32.
+ * Workspace: ogn_segment_reduce_workspace_size(batch, length, segments, k, 1,
+ * dtype, OGN_REDUCE_LSE).  First pass of scatter_softmax / scatter_log_softmax
+ * on a sorted index (reference csrc/npu/scatter_softmax/common/grouped_softmax_shared.h:178-209
+ * phases 1-2). */
+int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
+                            int64_t segments, int64_t k, float* m_out, float* s_out, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ unsorted scatter
+ * torch_scatter scatter with an arbitrary int64 index (same rules as
+ * OGN_SEM_SCATTER above).  src: [before, len, after] contiguous; index read
+ * at b*index_stride_before + l*index_stride_len + f*index_stride_after
+ * (strides in elements, 0 = broadcast); out/arg: [before, size, after]; when
+ * has_out, out holds the starting values.  reduce: sum, mean, min, max,
+ * prod.  arg (int64) is required for min/max.  Entries of index outside
+ * [0, size) are skipped.  fp32 atomics: sum/mean/prod order may vary between
+ * runs; min/max and arg are exact.  Replaces scatter_forward
+ * (reference csrc/npu/scatter/op_host/scatter.cpp:242-269) and its atomic and
+ * min/max kernels (csrc/npu/scatter/op_kernel/arch35/scatter_kernel_atomic.h:338-412,
+ * scatter_kernel_minmax.h:120-175). */
+size_t ogn_scatter_atomic_workspace_size(int64_t before, int64_t size, int64_t after, int reduce);
+int ogn_scatter_atomic(const void* src, int dtype, const int64_t* index, int64_t index_stride_before,
+                       int64_t index_stride_len, int64_t index_stride_after, int64_t before, int64_t len,
+                       int64_t after, int64_t size, void* out, int64_t* arg, int reduce, int has_out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ grouped softmax
+ * Groups = positions l along the reduction dim sharing index[l] (1-D int32 or
+ * int64 index of length len); src/out [before, len, after].
+ * ogn_group_stats_atomic: m/s statistics as ogn_segment_group_stats for an
+ *   unsorted index, with atomics (m, s: [before, groups, after] fp32;
+ *   scratch_key: same size, uint32).
+ * ogn_group_softmax_apply: out = exp(x - m') / s (softmax) or
+ *   (x - m') - log(s) (log_softmax), m' = clamp(m, +-FLT_MAX); NaN for a group
+ *   holding +inf; positions whose index is outside [0, groups) get 0.
+ * ogn_group_lse_from_stats: out = m' + log(s) over `cells` entries.
+ * Replace the three-phase RunForward of the reference
+ * (csrc/npu/scatter_softmax/common/grouped_softmax_shared.h:178-209,
+ * csrc/npu/scatter_logsumexp/common/grouped_logsumexp_shared.h:50-90). */
+int ogn_group_stats_atomic(const void* src, int dtype, const void* index, int index_dtype, int64_t before,
+                           int64_t len, int64_t after, int64_t groups, float* m, float* s, uint32_t* scratch_key,
+                           void* stream);
+int ogn_group_softmax_apply(const void* src, int dtype, const void* index, int index_dtype, int64_t before,
+                            int64_t len, int64_t after, int64_t groups, const float* m, const float* s,
+                            void* out, int log_softmax, void* stream);
+int ogn_group_lse_from_stats(const float* m, const float* s, int64_t cells, void* out, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,634 @@
+// CSR reduction engine for gfx950: the one kernel family behind CSR SpMM,
+// segment_csr, segment_coo, sorted-index scatter and segment log-sum-exp.
+//
+//   out[b, r, k] = R_{e in [ptr[r], ptr[r+1])} w(e, k) * x[b, row(e), k]
+//
+// row(e) = col[e] (gather mode, SpMM) or e itself (contiguous mode: segment
+// reductions, where each segment is a run of consecutive rows of src).
+// R = sum / mean / prod, min / max (+ arg), or log-sum-exp.
+//
+// Schedule: nnz-split.  The position range [ptr[0], ptr[m]) is cut into
+// chunks of C positions and one wavefront owns one chunk, so every wave does
+// the same amount of work whatever the row-length distribution (power-law
+// hub rows are spread over many waves; runs of short rows share one).
+//
+// Inside a wave the 64 lanes form S = 64 / G sub-groups of G lanes; a
+// sub-group covers one feature row with one 16-byte load per lane (vector
+// mode, G = K * sizeof(T) / 16) or one element per lane (scalar mode), so a
+// step touches S positions and U steps are in flight before any is consumed.
+// Column indices and edge weights are staged with one coalesced load per 64
+// positions and handed to the sub-groups with ds_bpermute; row ends come
+// from a 64-row window of the pointer array held one entry per lane.
+//
+// Ownership: a row is finished by the chunk holding its last position (empty
+// rows by the chunk their position falls in).  A row crossing a chunk
+// boundary leaves partial records -- "tail" in each chunk it leaves, "head"
+// in the chunk where it ends -- and a fix-up kernel folds
+// tail[c1..c2-1] + head[c2] in chunk order and finishes the row.  Results are
+// deterministic (no atomics; fixed combination order).
+#pragma once
+
+#include "ogn_device.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace ogn {
+namespace eng {
+
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kUnroll = 8;
+constexpr int64_t kNone = INT64_MAX;
+
+// Reduction kinds (template parameter RK).
+enum { RK_SUM = 0, RK_MINMAX = 1, RK_LSE = 2 };
+
+// Extremum finishing rules.
+enum {
+  MM_SPMM = 0,    // torch_sparse: NaN ignored, first tie, none -> 0 / arg_empty
+  MM_SEGCSR = 1,  // segment_csr: strict improvement from +-inf (arg = segment start)
+  MM_LATER = 2    // segment_coo / scatter: fold from a seed with >= / <=, later tie
+};
+// Seeds for MM_LATER.
+enum {
+  SEED_NONE = 0,
+  SEED_OUT = 1,    // the current value of out (arg = arg_empty)
+  SEED_FIRST = 2,  // the first element of the segment (arg = its position)
+  SEED_LIMIT = 3   // +-limit (finite dtype extreme); still the seed at the end -> 0
+};
+
+struct Params {
+  const void* ptr;
+  int64_t ptr_bstride;  // elements between the pointer rows of batches (0 = shared)
+  const void* col;      // gather mode
+  const void* val;
+  int val_mode;         // 0 none, 1 one weight per position, 2 k weights per position
+  const void* src;
+  int src_dt;
+  int64_t src_bstride;  // elements between batches of src
+  void* out;
+  int out_dt;
+  int64_t out_bstride;  // elements between batches of out
+  int64_t* arg;
+  int64_t* chunk_row;   // [ptr batches][nchunks]
+  void* rec_head;       // [batch][nchunks][k] partial values
+  void* rec_tail;
+  int64_t* arg_head;    // [batch][nchunks][k] partial args (min/max)
+  int64_t* arg_tail;
+  int64_t m;            // rows of the output (segments)
+  int64_t n;            // rows of src addressable (gather bound / length)
+  int64_t k;            // features
+  int64_t nnz_bound;    // host bound on ptr[m] - ptr[0] (sizes the grid)
+  int64_t chunk;
+  int64_t nchunks;
+  int reduce;           // OGN_REDUCE_*
+  int mm_mode;
+  int seed_mode;
+  int sum_seed;         // sum / mean start from the current out value
+  int mean_keep_empty;  // mean of an empty row keeps the seed (else 0)
+  float limit;
+  int64_t arg_empty;
+  float* aux;           // log-sum-exp statistics mode: out <- max, aux <- sum of exp
+};
+
+template <typename MT>
+__device__ __forceinline__ bool better(MT v, MT best, bool is_min) {
+  return is_min ? v < best : v > best;
+}
+
+__device__ __forceinline__ float clampf_max(float m) {
+  return fminf(fmaxf(m, -3.402823466e38f), 3.402823466e38f);
+}
+
+// Log-sum-exp state merge: (m, s) = running max and sum of exp(x - clamp(m)).
+__device__ __forceinline__ void lse_merge(float& m, float& s, float om, float os) {
+  const float nm = fmaxf(m, om);
+  const float cn = clampf_max(nm);
+  const float a = s == 0.f ? 0.f : s * expf(clampf_max(m) - cn);
+  const float bb = os == 0.f ? 0.f : os * expf(clampf_max(om) - cn);
+  m = nm;
+  s = a + bb;
+}
+
+__device__ __forceinline__ void lse_add(float& m, float& s, float x) {
+  if (x > m) {
+    const float cn = clampf_max(x);
+    s = (s == 0.f ? 0.f : s * expf(clampf_max(m) - cn)) + expf(x - cn);
+    m = x;
+  } else {
+    s += expf(x - clampf_max(m));
+  }
+}
+
+// Finish one output element from its combined partial state.
+//   sum kinds: a = sum (or product); mean divides by the row length.
+//   min/max: (best, barg) resolved against the seed of the mode.
+//   lse: (best = m, a = s).
+template <int RK, typename MT>
+__device__ __forceinline__ void finish_elem(const Params& p, int64_t b, int64_t r, int64_t k,
+                                            int64_t rs, int64_t re, float a, MT best, int64_t barg,
+                                            float* outv, int64_t* outarg) {
+  const int64_t off = b * p.out_bstride + r * p.k + k;
+  const int64_t cnt = re - rs;
+  if constexpr (RK == RK_SUM) {
+    float v = a;
+    if (p.sum_seed) {
+      const float seed = load_float(p.out, p.out_dt, off);
+      v = p.reduce == OGN_REDUCE_PROD ? seed * v : seed + v;
+    }
+    if (p.reduce == OGN_REDUCE_MEAN) {
+      if (cnt > 0) v = v / (float)cnt;
+      else v = p.mean_keep_empty ? load_float(p.out, p.out_dt, off) : 0.f;
+    }
+    *outv = v;
+  } else if constexpr (RK == RK_LSE) {
+    if (p.aux) {
+      *outv = cnt > 0 ? (float)best : -__builtin_inff();
+      p.aux[off] = cnt > 0 ? a : 0.f;
+    } else {
+      *outv = cnt > 0 ? clampf_max(best) + logf(a) : -__builtin_inff();
+    }
+  } else {
+    const bool is_min = p.reduce == OGN_REDUCE_MIN;
+    const bool has = barg != kNone;
+    if (p.mm_mode == MM_SPMM) {
+      *outv = has ? (float)best : 0.f;
+      *outarg = has ? barg : p.arg_empty;
+    } else if (p.mm_mode == MM_SEGCSR) {
+      if (cnt <= 0) {
+        *outv = 0.f;
+        *outarg = p.arg_empty;
+      } else {
+        const MT sentinel = is_min ? (MT)__builtin_inff() : (MT)-__builtin_inff();
+        const bool take = has && better(best, sentinel, is_min);
+        *outv = take ? (float)best : (float)sentinel;
+        *outarg = take ? barg : rs;
+      }
+    } else {
+      MT sv;
+      int64_t sa = p.arg_empty;
+      if (p.seed_mode == SEED_OUT) {
+        sv = (MT)load_float(p.out, p.out_dt, off);
+      } else if (p.seed_mode == SEED_FIRST) {
+        if (cnt <= 0) {
+          *outv = 0.f;
+          *outarg = p.arg_empty;
+          return;
+        }
+        sv = (MT)load_float(p.src, p.src_dt, b * p.src_bstride + rs * p.k + k);
+        sa = rs;
+      } else {
+        sv = is_min ? (MT)p.limit : (MT)-p.limit;
+      }
+      const bool take = has && !(sv != sv) && (is_min ? best <= sv : best >= sv);
+      float v = take ? (float)best : (float)sv;
+      const int64_t ra = take ? barg : sa;
+      if (p.seed_mode == SEED_LIMIT && ra == p.arg_empty) v = 0.f;
+      *outv = v;
+      *outarg = ra;
+    }
+  }
+}
+
+// Row ids of the first position of every chunk: row r owns the chunk starts
+// that fall inside [ptr[r], ptr[r+1]).
+template <typename IDX>
+__global__ __launch_bounds__(256) void chunk_rows_kernel(Params p) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= p.m) return;
+  const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr) + blockIdx.y * p.ptr_bstride;
+  const int64_t base = ptr[0];
+  const int64_t a = (int64_t)ptr[r] - base, z = (int64_t)ptr[r + 1] - base;
+  if (z <= a) return;
+  int64_t c0 = (a + p.chunk - 1) / p.chunk, c1 = (z - 1) / p.chunk;
+  c0 = std::max<int64_t>(c0, 0);
+  c1 = std::min<int64_t>(c1, p.nchunks - 1);
+  int64_t* __restrict__ cr = p.chunk_row + blockIdx.y * p.nchunks;
+  for (int64_t c = c0; c <= c1; ++c) cr[c] = r;
+}
+
+template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER>
+__global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
+  using E = Elem<DT>;
+  using S_t = typename E::S;
+  constexpr int NE = VL ? E::VEC : 1;
+  constexpr int S = kWave / G;
+  // min/max of fp32 compare exact fp64 products; fp16/bf16 products are exact in fp32.
+  using MT = std::conditional_t<RK == RK_MINMAX && DT == OGN_F32, double, float>;
+
+  const int lane = lane_id();
+  const int sub = lane / G;
+  const int gl = lane % G;
+  const int64_t c = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (c >= p.nchunks) return;
+  const int64_t b = blockIdx.z;
+  const int64_t pb = p.ptr_bstride ? b : 0;
+  const int64_t K = p.k;
+  const int64_t M = p.m;
+  const int64_t k0 = (int64_t)blockIdx.y * (G * NE) + gl * NE;
+  const bool kok = VL || k0 < K;
+  const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr) + pb * p.ptr_bstride;
+  const IDX* __restrict__ col = static_cast<const IDX*>(p.col);
+  const S_t* __restrict__ srcb = static_cast<const S_t*>(p.src) + b * p.src_bstride;
+  const S_t* __restrict__ val = static_cast<const S_t*>(p.val);
+  const bool is_min = p.reduce == OGN_REDUCE_MIN;
+  const bool is_prod = p.reduce == OGN_REDUCE_PROD;
+  const bool later = p.mm_mode == MM_LATER;
+
+  const int64_t base = ptr[0];
+  const int64_t end = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[M] - base, p.nnz_bound), 0);
+  const int64_t nce = std::max<int64_t>(1, (end + p.chunk - 1) / p.chunk);
+  if (c >= nce) return;
+  const int64_t lo = base + c * p.chunk;
+  const int64_t hi = base + std::min<int64_t>((c + 1) * p.chunk, end);
+  int64_t r = c == 0 ? 0 : std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c], 0), M - 1);
+
+  // Pointer window: lane j holds ptr[wb + 1 + j].
+  int64_t wb = r;
+  IDX pw = ptr[std::min<int64_t>(wb + 1 + lane, M)];
+  auto rowend = [&](int64_t rr) -> int64_t {
+    if (rr >= M) return kNone;
+    if (rr - wb >= kWave) {
+      wb = rr;
+      pw = ptr[std::min<int64_t>(wb + 1 + lane, M)];
+    }
+    return (int64_t)readlane64(pw, (int)(rr - wb));
+  };
+  int64_t rs = (int64_t)ptr[r];
+  int64_t re = rowend(r);
+  const bool head_split = rs < lo;
+  bool first = true;
+
+  float acc[NE];
+  MT best[NE];
+  int64_t barg[NE];
+  auto reset = [&]() {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      acc[i] = is_prod ? 1.f : 0.f;
+      best[i] = RK == RK_LSE ? (MT)-__builtin_inff() : (MT)0;
+      barg[i] = kNone;
+    }
+  };
+  reset();
+
+  // Combine the S sub-group partials of the current row; all lanes end with
+  // the combined state.  Lower sub-groups hold earlier positions.
+  auto combine = [&]() {
+#pragma unroll
+    for (int off = G; off < kWave; off <<= 1) {
+      const bool upper = (lane & off) != 0;  // partner holds earlier positions
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        if constexpr (RK == RK_MINMAX) {
+          const MT ob = (MT)(sizeof(MT) == 8 ? shfld((double)best[i], lane ^ off)
+                                             : shflf((float)best[i], lane ^ off));
+          const int64_t oa = shfl64(barg[i], lane ^ off);
+          bool take;
+          if (later) {
+            take = oa != kNone && (barg[i] == kNone || better(ob, best[i], is_min) ||
+                                   (ob == best[i] && oa > barg[i]));
+          } else {
+            take = oa != kNone && (barg[i] == kNone || better(ob, best[i], is_min) ||
+                                   (ob == best[i] && oa < barg[i]));
+          }
+          if (take) {
+            best[i] = ob;
+            barg[i] = oa;
+          }
+        } else if constexpr (RK == RK_LSE) {
+          const float om = shflf((float)best[i], lane ^ off);
+          const float os = shflf(acc[i], lane ^ off);
+          // merge in position order so every lane computes the same value
+          float m1 = upper ? om : (float)best[i], s1 = upper ? os : acc[i];
+          const float m2 = upper ? (float)best[i] : om, s2 = upper ? acc[i] : os;
+          lse_merge(m1, s1, m2, s2);
+          best[i] = m1;
+          acc[i] = s1;
+        } else {
+          const float o = shflf(acc[i], lane ^ off);
+          const float lo_v = upper ? o : acc[i], hi_v = upper ? acc[i] : o;
+          acc[i] = is_prod ? lo_v * hi_v : lo_v + hi_v;
+        }
+      }
+    }
+  };
+
+  auto write_record = [&](bool head) {
+    if (sub != 0 || !kok) return;
+    const int64_t rb = (b * p.nchunks + c) * K + k0;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      if (!VL && k0 + i >= K) break;
+      if constexpr (RK == RK_MINMAX) {
+        static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)best[i];
+        (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i];
+      } else if constexpr (RK == RK_LSE) {
+        static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2((float)best[i], acc[i]);
+      } else {
+        static_cast<float*>(head ? p.rec_head : p.rec_tail)[rb + i] = acc[i];
+      }
+    }
+  };
+
+  auto flush = [&]() {
+    combine();
+    if (head_split && first) {
+      write_record(true);
+    } else if (sub == 0 && kok) {
+      float v[NE];
+      int64_t ag[NE];
+#pragma unroll
+      for (int i = 0; i < NE; ++i)
+        finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, acc[i], best[i], barg[i], &v[i], &ag[i]);
+      const int64_t off = b * p.out_bstride + r * K + k0;
+      if (VL || k0 + NE <= K) {
+        store_floats<NE>(p.out, p.out_dt, off, v);
+      }
+      if constexpr (RK == RK_MINMAX) {
+        if (p.arg) {
+#pragma unroll
+          for (int i = 0; i < NE; ++i) p.arg[off + i] = ag[i];
+        }
+      }
+    }
+    first = false;
+    reset();
+  };
+
+  for (int64_t wbase = lo; wbase < hi; wbase += kWave) {
+    const int64_t el = wbase + lane;
+    const bool ev = el < hi;
+    int64_t cl;
+    if constexpr (GATHER) {
+      cl = ev ? (int64_t)load_stream(col + el) : 0;
+    } else {
+      cl = el;
+    }
+    cl = std::min<int64_t>(std::max<int64_t>(cl, 0), p.n - 1);
+    float vl = 1.f;
+    if (p.val_mode == 1) vl = ev ? E::load1(val, el) : 0.f;
+    const int nw = (int)std::min<int64_t>(kWave, hi - wbase);
+    const int nsteps = (nw + S - 1) / S;
+    for (int j0 = 0; j0 < nsteps; j0 += kUnroll) {
+      float x[kUnroll][NE];
+      float w[kUnroll][VL ? NE : 1];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int idx = (j0 + u) * S + sub;
+        int64_t cc;
+        if constexpr (GATHER) {
+          cc = (int64_t)shfl64((IDX)cl, idx & (kWave - 1));
+        } else {
+          cc = std::min<int64_t>(wbase + idx, p.n - 1);
+        }
+        const float ws = p.val_mode == 1 ? shflf(vl, idx & (kWave - 1)) : 1.f;
+        const bool ok = (j0 + u) < nsteps && idx < nw && kok;
+        if constexpr (VL) {
+          if (ok) {
+            E::unpack(load16(srcb + cc * K + k0), x[u]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < NE; ++i) x[u][i] = 0.f;
+          }
+#pragma unroll
+          for (int i = 0; i < NE; ++i) w[u][i] = ws;
+          if (p.val_mode == 2 && ok) {
+            float wv[NE];
+            E::unpack(load16(val + (wbase + idx) * K + k0), wv);
+#pragma unroll
+            for (int i = 0; i < NE; ++i) w[u][i] = wv[i];
+          }
+        } else {
+          x[u][0] = ok ? E::load1(srcb, cc * K + k0) : 0.f;
+          w[u][0] = ws;
+          if (p.val_mode == 2 && ok) w[u][0] = E::load1(val, (wbase + idx) * K + k0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (j0 + u >= nsteps) break;
+        const int64_t e_first = wbase + (int64_t)(j0 + u) * S;
+        const int64_t last = std::min<int64_t>(e_first + S, hi) - 1;
+        const int64_t e_mine = e_first + sub;
+        const bool valid = e_mine < hi;
+        bool added = false;
+        while (true) {
+          if (!added && valid && e_mine < re) {
+#pragma unroll
+            for (int i = 0; i < NE; ++i) {
+              const float wi = w[u][VL ? i : 0];
+              if constexpr (RK == RK_MINMAX) {
+                const MT pv = (MT)x[u][i] * (MT)wi;
+                if (!(pv != pv)) {
+                  const bool take = barg[i] == kNone || better(pv, best[i], is_min) ||
+                                    (later && pv == best[i]);
+                  if (take) {
+                    best[i] = pv;
+                    barg[i] = e_mine;
+                  }
+                }
+              } else if constexpr (RK == RK_LSE) {
+                float m = (float)best[i];
+                lse_add(m, acc[i], x[u][i] * wi);
+                best[i] = m;
+              } else {
+                acc[i] = is_prod ? acc[i] * (x[u][i] * wi) : __builtin_fmaf(x[u][i], wi, acc[i]);
+              }
+            }
+            added = true;
+          }
+          if (last < re) break;
+          flush();
+          ++r;
+          rs = re;
+          re = rowend(r);
+        }
+      }
+    }
+  }
+  // Rows that end exactly at `hi` and the empty rows behind them.
+  while (r < M && re <= hi) {
+    flush();
+    ++r;
+    rs = re;
+    re = rowend(r);
+  }
+  if (r < M && rs < hi) {
+    combine();
+    write_record(false);
+  }
+}
+
+// Finish rows that cross chunk boundaries: one wave per chunk that holds the
+// first piece of such a row; loads of the partial records are issued in
+// groups of 8 and folded in chunk order.
+template <typename IDX, int RK, bool F32MM>
+__global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
+  using MT = std::conditional_t<F32MM, double, float>;
+  const int lane = lane_id();
+  const int64_t c = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t b = blockIdx.z;
+  const int64_t pb = p.ptr_bstride ? b : 0;
+  const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr) + pb * p.ptr_bstride;
+  const int64_t base = ptr[0];
+  const int64_t end = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[p.m] - base, p.nnz_bound), 0);
+  const int64_t nce = std::max<int64_t>(1, (end + p.chunk - 1) / p.chunk);
+  if (c + 1 >= nce) return;
+  const int64_t lo = base + c * p.chunk, hi = lo + p.chunk;
+  const int64_t r = std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c + 1], 0), p.m - 1);
+  const int64_t rs = ptr[r];
+  if (!(rs < hi && rs >= lo)) return;
+  const int64_t re = ptr[r + 1];
+  const int64_t c2 = std::min<int64_t>((re - 1 - base) / p.chunk, nce - 1);
+  const int64_t K = p.k;
+  const bool is_min = p.reduce == OGN_REDUCE_MIN;
+  const bool is_prod = p.reduce == OGN_REDUCE_PROD;
+  const bool later = p.mm_mode == MM_LATER;
+  constexpr int kBatch = 8;
+  for (int64_t k = lane; k < K; k += kWave) {
+    const int64_t base_rec = (b * p.nchunks) * K + k;
+    float a = 0.f;
+    MT best = 0;
+    int64_t barg = kNone;
+    if constexpr (RK == RK_MINMAX) {
+      best = (MT)static_cast<const double*>(p.rec_tail)[base_rec + c * K];
+      barg = p.arg_tail[base_rec + c * K];
+    } else if constexpr (RK == RK_LSE) {
+      const float2 t = static_cast<const float2*>(p.rec_tail)[base_rec + c * K];
+      best = t.x;
+      a = t.y;
+    } else {
+      a = static_cast<const float*>(p.rec_tail)[base_rec + c * K];
+    }
+    for (int64_t c0 = c + 1; c0 <= c2; c0 += kBatch) {
+      float va[kBatch], vb[kBatch];
+      double vd[kBatch];
+      int64_t vg[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int64_t cc = c0 + j;
+        const bool ok = cc <= c2;
+        const int64_t ri = base_rec + std::min<int64_t>(cc, c2) * K;
+        const bool head = cc >= c2;
+        if constexpr (RK == RK_MINMAX) {
+          vd[j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
+          vg[j] = ok ? (head ? p.arg_head : p.arg_tail)[ri] : kNone;
+        } else if constexpr (RK == RK_LSE) {
+          const float2 t = ok ? static_cast<const float2*>(head ? p.rec_head : p.rec_tail)[ri]
+                              : make_float2(-__builtin_inff(), 0.f);
+          va[j] = t.x;
+          vb[j] = t.y;
+        } else {
+          va[j] = ok ? static_cast<const float*>(head ? p.rec_head : p.rec_tail)[ri] : (is_prod ? 1.f : 0.f);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if constexpr (RK == RK_MINMAX) {
+          const MT ob = (MT)vd[j];
+          const int64_t oa = vg[j];
+          // later records hold later positions
+          if (oa != kNone && (barg == kNone || better(ob, best, is_min) || (later && ob == best))) {
+            best = ob;
+            barg = oa;
+          }
+        } else if constexpr (RK == RK_LSE) {
+          float m = (float)best;
+          lse_merge(m, a, va[j], vb[j]);
+          best = m;
+        } else {
+          a = is_prod ? a * va[j] : a + va[j];
+        }
+      }
+    }
+    float v;
+    int64_t ag = 0;
+    finish_elem<RK, MT>(p, b, r, k, rs, re, a, best, barg, &v, &ag);
+    const int64_t off = b * p.out_bstride + r * K + k;
+    store_floats<1>(p.out, p.out_dt, off, &v);
+    if constexpr (RK == RK_MINMAX) {
+      if (p.arg) p.arg[off] = ag;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host side
+struct Plan {
+  bool vec;
+  int g;
+  int64_t tiles;
+  int64_t chunk;
+  int64_t nchunks;
+};
+
+Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned);
+
+struct Workspace {
+  size_t chunk_row, head, tail, arg_head, arg_tail, total;
+};
+
+Workspace workspace_layout(const Plan& pl, int64_t k, int64_t batch, int64_t ptr_batches, int rk);
+
+// Run the engine: chunk-row pass, main pass, fix-up pass.  `name` labels the
+// launches for the opt-in timer (<name>_main etc.).
+int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, int rk, int64_t batch,
+        void* workspace, size_t workspace_bytes, hipStream_t s, const char* name);
+
+// Per-dtype / per-mode instantiations (engine_<mode>_<dt>.hip).
+#define OGN_ENGINE_DECL(NAME) \
+  void NAME(const Plan&, int rk, bool i64, dim3, hipStream_t, const Params&);
+OGN_ENGINE_DECL(launch_gather_f32)
+OGN_ENGINE_DECL(launch_gather_f16)
+OGN_ENGINE_DECL(launch_gather_bf16)
+OGN_ENGINE_DECL(launch_contig_f32)
+OGN_ENGINE_DECL(launch_contig_f16)
+OGN_ENGINE_DECL(launch_contig_bf16)
+#undef OGN_ENGINE_DECL
+
+template <int DT, typename IDX, bool VL, int RK, bool GATHER>
+void launch_g(int g, dim3 grid, hipStream_t s, const Params& p) {
+  switch (g) {
+#define OGN_G(GV) \
+  case GV: hipLaunchKernelGGL((engine_kernel<DT, IDX, GV, VL, RK, GATHER>), grid, dim3(kBlock), 0, s, p); break;
+    OGN_G(1) OGN_G(2) OGN_G(4) OGN_G(8) OGN_G(16) OGN_G(32) OGN_G(64)
+#undef OGN_G
+    default: break;
+  }
+}
+
+template <int DT, typename IDX, int RK, bool GATHER>
+void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
+  if (pl.vec) {
+    launch_g<DT, IDX, true, RK, GATHER>(pl.g, grid, s, p);
+  } else if (pl.g == 1) {
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 1, false, RK, GATHER>), grid, dim3(kBlock), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 64, false, RK, GATHER>), grid, dim3(kBlock), 0, s, p);
+  }
+}
+
+// Gather mode (SpMM) instantiates int32 and int64 indices with sum / min-max;
+// contiguous mode (segments) uses int64 pointers with every reduction kind.
+template <int DT>
+void launch_gather_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
+  if (rk == RK_MINMAX) {
+    i64 ? launch_rk<DT, int64_t, RK_MINMAX, true>(pl, grid, s, p)
+        : launch_rk<DT, int32_t, RK_MINMAX, true>(pl, grid, s, p);
+  } else {
+    i64 ? launch_rk<DT, int64_t, RK_SUM, true>(pl, grid, s, p)
+        : launch_rk<DT, int32_t, RK_SUM, true>(pl, grid, s, p);
+  }
+}
+
+template <int DT>
+void launch_contig_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
+  (void)i64;  // segment pointers are int64
+  if (rk == RK_MINMAX) launch_rk<DT, int64_t, RK_MINMAX, false>(pl, grid, s, p);
+  else if (rk == RK_LSE) launch_rk<DT, int64_t, RK_LSE, false>(pl, grid, s, p);
+  else launch_rk<DT, int64_t, RK_SUM, false>(pl, grid, s, p);
+}
+
+}  // namespace eng
+}  // namespace ogn

@@ -1,0 +1,127 @@
+// Host side of the CSR reduction engine: launch geometry, workspace layout
+// and the three-pass launch sequence (chunk rows, main, fix-up).
+#include "csr_engine.h"
+
+#include <cstdlib>
+#include <string>
+
+namespace ogn {
+namespace eng {
+
+Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned) {
+  Plan pl{};
+  const int esz = dtype_size(in_dtype);
+  const int vec = 16 / esz;
+  const int64_t kv = k / vec;
+  if (aligned && k % vec == 0 && kv <= 64 && (kv & (kv - 1)) == 0) {
+    pl.vec = true;
+    pl.g = (int)kv;
+    pl.tiles = 1;
+  } else if (aligned && k % vec == 0 && kv % 64 == 0) {
+    pl.vec = true;
+    pl.g = 64;
+    pl.tiles = kv / 64;
+  } else if (k == 1) {
+    pl.vec = false;  // one feature: 64 positions per step, one per lane
+    pl.g = 1;
+    pl.tiles = 1;
+  } else {
+    pl.vec = false;
+    pl.g = 64;
+    pl.tiles = (k + 63) / 64;
+  }
+  // About 128 KiB of feature traffic per wave, in whole 64-position windows.
+  const int64_t row_bytes = std::max<int64_t>(1, std::min<int64_t>(k, 64 * vec) * esz);
+  int64_t chunk = (131072 / row_bytes + 63) / 64 * 64;
+  if (const char* env = std::getenv("OGN_ENGINE_CHUNK")) {
+    const long v = std::atol(env);
+    if (v >= 64) chunk = v / 64 * 64;
+  }
+  pl.chunk = std::min<int64_t>(std::max<int64_t>(chunk, 64), 8192);
+  pl.nchunks = std::max<int64_t>(1, (nnz_bound + pl.chunk - 1) / pl.chunk);
+  return pl;
+}
+
+static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+Workspace workspace_layout(const Plan& pl, int64_t k, int64_t batch, int64_t ptr_batches, int rk) {
+  Workspace w{};
+  const size_t rec = (size_t)pl.nchunks * batch * k;
+  w.chunk_row = 0;
+  w.head = align256(sizeof(int64_t) * pl.nchunks * ptr_batches);
+  const size_t vsz = rk == RK_SUM ? sizeof(float) : (rk == RK_LSE ? sizeof(float2) : sizeof(double));
+  const size_t vbytes = align256(rec * vsz);
+  w.tail = w.head + vbytes;
+  w.arg_head = w.tail + vbytes;
+  const size_t abytes = rk == RK_MINMAX ? align256(rec * sizeof(int64_t)) : 0;
+  w.arg_tail = w.arg_head + abytes;
+  w.total = w.arg_tail + abytes;
+  return w;
+}
+
+int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, int rk, int64_t batch,
+        void* workspace, size_t workspace_bytes, hipStream_t s, const char* name) {
+  const int64_t ptr_batches = p.ptr_bstride ? batch : 1;
+  const Workspace wl = workspace_layout(pl, p.k, batch, ptr_batches, rk);
+  if (!workspace || workspace_bytes < wl.total)
+    return fail(OGN_EINVAL, std::string(name) + ": workspace too small (need " +
+                                std::to_string(wl.total) + " bytes)");
+  if (batch > 65535 || pl.tiles > 65535)
+    return fail(OGN_EUNSUPPORTED, std::string(name) + ": batch or feature tiles exceed 65535");
+  char* ws = static_cast<char*>(workspace);
+  p.chunk_row = reinterpret_cast<int64_t*>(ws + wl.chunk_row);
+  p.rec_head = ws + wl.head;
+  p.rec_tail = ws + wl.tail;
+  p.arg_head = rk == RK_MINMAX ? reinterpret_cast<int64_t*>(ws + wl.arg_head) : nullptr;
+  p.arg_tail = rk == RK_MINMAX ? reinterpret_cast<int64_t*>(ws + wl.arg_tail) : nullptr;
+  p.chunk = pl.chunk;
+  p.nchunks = pl.nchunks;
+  const bool i64 = index_dtype == OGN_I64;
+  const std::string n(name);
+  {
+    TimedLaunch t((n + "_chunk_rows").c_str(), s);
+    const dim3 g((unsigned)((p.m + 255) / 256), (unsigned)ptr_batches);
+    if (i64) hipLaunchKernelGGL(chunk_rows_kernel<int64_t>, g, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(chunk_rows_kernel<int32_t>, g, dim3(256), 0, s, p);
+  }
+  const dim3 grid((unsigned)((pl.nchunks + kWavesPerBlock - 1) / kWavesPerBlock), (unsigned)pl.tiles,
+                  (unsigned)batch);
+  {
+    TimedLaunch t((n + "_main").c_str(), s);
+    switch (in_dtype) {
+      case OGN_F32:
+        gather ? launch_gather_f32(pl, rk, i64, grid, s, p) : launch_contig_f32(pl, rk, i64, grid, s, p);
+        break;
+      case OGN_F16:
+        gather ? launch_gather_f16(pl, rk, i64, grid, s, p) : launch_contig_f16(pl, rk, i64, grid, s, p);
+        break;
+      default:
+        gather ? launch_gather_bf16(pl, rk, i64, grid, s, p) : launch_contig_bf16(pl, rk, i64, grid, s, p);
+        break;
+    }
+  }
+  if (pl.nchunks > 1) {
+    TimedLaunch t((n + "_fixup").c_str(), s);
+    const dim3 fg((unsigned)((pl.nchunks + kWavesPerBlock - 1) / kWavesPerBlock), 1, (unsigned)batch);
+    const bool f32mm = rk == RK_MINMAX && in_dtype == OGN_F32;
+#define OGN_FIX(IDX)                                                                          \
+  switch (rk) {                                                                               \
+    case RK_MINMAX:                                                                           \
+      if (f32mm) hipLaunchKernelGGL((fixup_kernel<IDX, RK_MINMAX, true>), fg, dim3(kBlock), 0, s, p); \
+      else hipLaunchKernelGGL((fixup_kernel<IDX, RK_MINMAX, false>), fg, dim3(kBlock), 0, s, p);     \
+      break;                                                                                  \
+    case RK_LSE: hipLaunchKernelGGL((fixup_kernel<IDX, RK_LSE, false>), fg, dim3(kBlock), 0, s, p); break; \
+    default: hipLaunchKernelGGL((fixup_kernel<IDX, RK_SUM, false>), fg, dim3(kBlock), 0, s, p); break;     \
+  }
+    if (i64) {
+      OGN_FIX(int64_t)
+    } else {
+      OGN_FIX(int32_t)
+    }
+#undef OGN_FIX
+  }
+  return check_launch(name);
+}
+
+}  // namespace eng
+}  // namespace ogn

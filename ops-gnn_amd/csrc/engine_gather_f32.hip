@@ -1,0 +1,12 @@
+// CSR engine instances: column-gather (SpMM) mode, f32 features.
+#include "csr_engine.h"
+
+namespace ogn {
+namespace eng {
+
+void launch_gather_f32(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
+  launch_gather_dt<OGN_F32>(pl, rk, i64, grid, s, p);
+}
+
+}  // namespace eng
+}  // namespace ogn

@@ -1,0 +1,410 @@
+// Unsorted-index scatter and the grouped-softmax passes for gfx950.
+//
+// scatter (torch_scatter rules) with an arbitrary index: one thread per src
+// element, fp32 accumulators in a workspace, hardware float atomics for
+// sum/mean, a compare-and-swap loop for prod, and an order-preserving
+// integer encoding of floats for min/max (atomic min/max on the key, then a
+// second pass records the largest position holding the winning value, which
+// is the "later writer wins" tie rule).  A finishing pass converts to the
+// output dtype.  Sum/mean/prod of floats are order-nondeterministic here (as
+// in any atomic scatter); the sorted-index path (segment engine) is exact.
+//
+// grouped softmax: per-(batch, group, feature) statistics m = max and
+// s = sum(exp(x - clamp(m))) -- from the segment engine when the index is
+// sorted, from atomics otherwise -- then one elementwise pass produces
+// softmax / log_softmax, or one pass over the groups produces logsumexp.
+#include "ogn_device.h"
+
+#include <algorithm>
+#include <string>
+
+namespace ogn {
+namespace {
+
+constexpr float kFltMax = 3.402823466e38f;
+
+__device__ __forceinline__ uint32_t key_of(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float float_of(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+__device__ __forceinline__ float clampm(float m) { return fminf(fmaxf(m, -kFltMax), kFltMax); }
+
+struct ScatterArgs {
+  const void* src;
+  int dt;
+  const int64_t* index;
+  int64_t isb, isl, isf;  // index strides over (before, len, after)
+  int64_t before, len, after, size;
+  void* out;
+  int64_t* arg;
+  float* acc;       // [before, size, after] fp32 accumulators (sum/mean/prod)
+  uint32_t* key;    // [before, size, after] min/max keys
+  int32_t* count;   // [before, size, after] mean counts
+  int reduce;
+  int has_out;
+  float limit;
+};
+
+__global__ __launch_bounds__(256) void scatter_init_kernel(ScatterArgs a) {
+  const int64_t total = a.before * a.size * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const float seed = a.has_out ? load_float(a.out, a.dt, i) : 0.f;
+    if (a.reduce == OGN_REDUCE_MIN || a.reduce == OGN_REDUCE_MAX) {
+      const bool is_min = a.reduce == OGN_REDUCE_MIN;
+      const float s0 = a.has_out ? seed : (is_min ? a.limit : -a.limit);
+      a.key[i] = key_of(s0 != s0 ? (is_min ? kFltMax : -kFltMax) : s0);
+      a.arg[i] = -1;  // no position taken yet
+    } else {
+      a.acc[i] = a.has_out ? seed : (a.reduce == OGN_REDUCE_PROD ? 1.f : 0.f);
+      if (a.count) a.count[i] = 0;
+    }
+  }
+}
+
+__device__ __forceinline__ void atomic_mul(float* p, float v) {
+  unsigned int* u = reinterpret_cast<unsigned int*>(p);
+  unsigned int old = __atomic_load_n(u, __ATOMIC_RELAXED);
+  while (true) {
+    const unsigned int want = __float_as_uint(__uint_as_float(old) * v);
+    if (__atomic_compare_exchange_n(u, &old, want, false, __ATOMIC_RELAXED, __ATOMIC_RELAXED)) break;
+  }
+}
+
+__global__ __launch_bounds__(256) void scatter_main_kernel(ScatterArgs a) {
+  const int64_t total = a.before * a.len * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t f = i % a.after;
+    const int64_t l = (i / a.after) % a.len;
+    const int64_t b = i / (a.after * a.len);
+    const int64_t t = a.index[b * a.isb + l * a.isl + f * a.isf];
+    if (t < 0 || t >= a.size) continue;
+    const float x = load_float(a.src, a.dt, i);
+    const int64_t o = (b * a.size + t) * a.after + f;
+    switch (a.reduce) {
+      case OGN_REDUCE_MIN:
+        if (!(x != x)) atomicMin(&a.key[o], key_of(x));
+        break;
+      case OGN_REDUCE_MAX:
+        if (!(x != x)) atomicMax(&a.key[o], key_of(x));
+        break;
+      case OGN_REDUCE_PROD:
+        atomic_mul(&a.acc[o], x);
+        break;
+      default:
+        atomicAdd(&a.acc[o], x);
+        if (a.count) atomicAdd(&a.count[o], 1);
+        break;
+    }
+  }
+}
+
+// Largest position whose value equals the final extremum (later writer wins).
+__global__ __launch_bounds__(256) void scatter_arg_kernel(ScatterArgs a) {
+  const int64_t total = a.before * a.len * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t f = i % a.after;
+    const int64_t l = (i / a.after) % a.len;
+    const int64_t b = i / (a.after * a.len);
+    const int64_t t = a.index[b * a.isb + l * a.isl + f * a.isf];
+    if (t < 0 || t >= a.size) continue;
+    const float x = load_float(a.src, a.dt, i);
+    if (x != x) continue;
+    const int64_t o = (b * a.size + t) * a.after + f;
+    if (float_of(a.key[o]) == x) atomicMax(reinterpret_cast<long long*>(&a.arg[o]), (long long)l);
+  }
+}
+
+__global__ __launch_bounds__(256) void scatter_finish_kernel(ScatterArgs a) {
+  const int64_t total = a.before * a.size * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    float v;
+    if (a.reduce == OGN_REDUCE_MIN || a.reduce == OGN_REDUCE_MAX) {
+      const float seed = a.has_out ? load_float(a.out, a.dt, i) : 0.f;
+      int64_t where = a.arg[i] < 0 ? a.len : a.arg[i];
+      if (a.has_out && seed != seed) {
+        v = seed;  // a NaN start value is never replaced
+        where = a.len;
+      } else if (where == a.len) {
+        v = seed;
+      } else {
+        const int64_t f = i % a.after;
+        const int64_t b = i / (a.after * a.size);
+        v = load_float(a.src, a.dt, (b * a.len + where) * a.after + f);
+      }
+      a.arg[i] = where;
+    } else {
+      v = a.acc[i];
+      if (a.reduce == OGN_REDUCE_MEAN) {
+        const int32_t c = a.count[i];
+        if (c > 0) v = v / (float)c;
+      }
+    }
+    store_floats<1>(a.out, a.dt, i, &v);
+  }
+}
+
+// ------------------------------------------------------------------ grouped softmax
+struct GroupArgs {
+  const void* src;
+  int dt;
+  const void* index;  // [len] int32 or int64
+  int idx64;
+  int64_t before, len, after, groups;
+  float* m;  // [before, groups, after]
+  float* s;
+  uint32_t* key;
+  void* out;
+  int mode;  // 0 softmax, 1 log_softmax
+};
+
+__device__ __forceinline__ int64_t group_of(const GroupArgs& a, int64_t l) {
+  return a.idx64 ? static_cast<const int64_t*>(a.index)[l] : (int64_t) static_cast<const int32_t*>(a.index)[l];
+}
+
+__global__ __launch_bounds__(256) void group_init_kernel(GroupArgs a) {
+  const int64_t total = a.before * a.groups * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    a.key[i] = key_of(-__builtin_inff());
+    a.s[i] = 0.f;
+  }
+}
+
+__global__ __launch_bounds__(256) void group_max_kernel(GroupArgs a) {
+  const int64_t total = a.before * a.len * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t f = i % a.after;
+    const int64_t l = (i / a.after) % a.len;
+    const int64_t b = i / (a.after * a.len);
+    const int64_t g = group_of(a, l);
+    if (g < 0 || g >= a.groups) continue;
+    const float x = load_float(a.src, a.dt, i);
+    if (!(x != x)) atomicMax(&a.key[(b * a.groups + g) * a.after + f], key_of(x));
+  }
+}
+
+__global__ __launch_bounds__(256) void group_sum_kernel(GroupArgs a) {
+  const int64_t total = a.before * a.len * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t f = i % a.after;
+    const int64_t l = (i / a.after) % a.len;
+    const int64_t b = i / (a.after * a.len);
+    const int64_t g = group_of(a, l);
+    if (g < 0 || g >= a.groups) continue;
+    const int64_t o = (b * a.groups + g) * a.after + f;
+    const float x = load_float(a.src, a.dt, i);
+    atomicAdd(&a.s[o], expf(x - clampm(float_of(a.key[o]))));
+  }
+}
+
+__global__ __launch_bounds__(256) void group_keys_to_max_kernel(GroupArgs a) {
+  const int64_t total = a.before * a.groups * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
+    a.m[i] = float_of(a.key[i]);
+}
+
+// softmax: exp(x - clamp(m)) / s;  log_softmax: (x - clamp(m)) - log(s).
+// A group holding +inf (m = +inf) is NaN throughout, as torch.softmax gives.
+__global__ __launch_bounds__(256) void group_apply_kernel(GroupArgs a) {
+  const int64_t total = a.before * a.len * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t f = i % a.after;
+    const int64_t l = (i / a.after) % a.len;
+    const int64_t b = i / (a.after * a.len);
+    const int64_t g = group_of(a, l);
+    float v = 0.f;
+    if (g >= 0 && g < a.groups) {
+      const int64_t o = (b * a.groups + g) * a.after + f;
+      const float m = a.m[o], s = a.s[o];
+      const float x = load_float(a.src, a.dt, i);
+      const float d = x - clampm(m);
+      v = a.mode == 0 ? expf(d) / s : d - logf(s);
+      if (m == __builtin_inff()) v = __builtin_nanf("");
+    }
+    store_floats<1>(a.out, a.dt, i, &v);
+  }
+}
+
+__global__ __launch_bounds__(256) void group_lse_kernel(GroupArgs a) {
+  const int64_t total = a.before * a.groups * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const float v = clampm(a.m[i]) + logf(a.s[i]);
+    store_floats<1>(a.out, a.dt, i, &v);
+  }
+}
+
+unsigned grid_for(int64_t total) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, 65536));
+}
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+}  // namespace
+}  // namespace ogn
+
+using namespace ogn;
+
+extern "C" {
+
+size_t ogn_scatter_atomic_workspace_size(int64_t before, int64_t size, int64_t after, int reduce) {
+  const size_t cells = (size_t)std::max<int64_t>(before, 0) * std::max<int64_t>(size, 0) * std::max<int64_t>(after, 0);
+  return align256(cells * 4) + (reduce == OGN_REDUCE_MEAN ? align256(cells * 4) : 0) + 256;
+}
+
+int ogn_scatter_atomic(const void* src, int dtype, const int64_t* index, int64_t index_stride_before,
+                       int64_t index_stride_len, int64_t index_stride_after, int64_t before, int64_t len,
+                       int64_t after, int64_t size, void* out, int64_t* arg, int reduce, int has_out,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (before < 0 || len < 0 || after < 0 || size < 0) return fail(OGN_EINVAL, "ogn_scatter_atomic: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_scatter_atomic: dtype must be float32, float16 or bfloat16");
+  if (reduce < OGN_REDUCE_SUM || reduce > OGN_REDUCE_PROD)
+    return fail(OGN_EINVAL, "ogn_scatter_atomic: reduce must be sum/mean/min/max/prod");
+  const int64_t cells = before * size * after;
+  if (cells == 0) return OGN_OK;
+  if (!out || (len > 0 && (!src || !index))) return fail(OGN_EINVAL, "ogn_scatter_atomic: null pointer");
+  if ((reduce == OGN_REDUCE_MIN || reduce == OGN_REDUCE_MAX) && !arg)
+    return fail(OGN_EINVAL, "ogn_scatter_atomic: min/max need an arg buffer");
+  if (!workspace || workspace_bytes < ogn_scatter_atomic_workspace_size(before, size, after, reduce))
+    return fail(OGN_EINVAL, "ogn_scatter_atomic: workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ScatterArgs a{};
+  a.src = src;
+  a.dt = dtype;
+  a.index = index;
+  a.isb = index_stride_before;
+  a.isl = index_stride_len;
+  a.isf = index_stride_after;
+  a.before = before;
+  a.len = len;
+  a.after = after;
+  a.size = size;
+  a.out = out;
+  a.arg = (reduce == OGN_REDUCE_MIN || reduce == OGN_REDUCE_MAX) ? arg : nullptr;
+  char* ws = static_cast<char*>(workspace);
+  a.acc = reinterpret_cast<float*>(ws);
+  a.key = reinterpret_cast<uint32_t*>(ws);
+  a.count = reduce == OGN_REDUCE_MEAN ? reinterpret_cast<int32_t*>(ws + align256(cells * 4)) : nullptr;
+  a.reduce = reduce;
+  a.has_out = has_out;
+  a.limit = dtype == OGN_F32 ? 3.4028234663852886e38f : (dtype == OGN_F16 ? 65504.f : 3.3895313892515355e38f);
+  {
+    TimedLaunch t("scatter_init", s);
+    hipLaunchKernelGGL(scatter_init_kernel, dim3(grid_for(cells)), dim3(256), 0, s, a);
+  }
+  const int64_t total = before * len * after;
+  if (total > 0) {
+    TimedLaunch t("scatter_main", s);
+    hipLaunchKernelGGL(scatter_main_kernel, dim3(grid_for(total)), dim3(256), 0, s, a);
+  }
+  if (a.arg != nullptr && total > 0) {
+    TimedLaunch t("scatter_arg", s);
+    hipLaunchKernelGGL(scatter_arg_kernel, dim3(grid_for(total)), dim3(256), 0, s, a);
+  }
+  {
+    TimedLaunch t("scatter_finish", s);
+    hipLaunchKernelGGL(scatter_finish_kernel, dim3(grid_for(cells)), dim3(256), 0, s, a);
+  }
+  return check_launch("ogn_scatter_atomic");
+}
+
+int ogn_group_stats_atomic(const void* src, int dtype, const void* index, int index_dtype, int64_t before,
+                           int64_t len, int64_t after, int64_t groups, float* m, float* s_out, uint32_t* scratch_key,
+                           void* stream) {
+  if (before < 0 || len < 0 || after < 0 || groups < 0)
+    return fail(OGN_EINVAL, "ogn_group_stats_atomic: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_group_stats_atomic: dtype must be float32, float16 or bfloat16");
+  if (index_dtype != OGN_I32 && index_dtype != OGN_I64)
+    return fail(OGN_EINVAL, "ogn_group_stats_atomic: index dtype must be int32 or int64");
+  const int64_t cells = before * groups * after;
+  if (cells == 0) return OGN_OK;
+  if (!m || !s_out || !scratch_key || (len > 0 && (!src || !index)))
+    return fail(OGN_EINVAL, "ogn_group_stats_atomic: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  GroupArgs a{};
+  a.src = src;
+  a.dt = dtype;
+  a.index = index;
+  a.idx64 = index_dtype == OGN_I64;
+  a.before = before;
+  a.len = len;
+  a.after = after;
+  a.groups = groups;
+  a.m = m;
+  a.s = s_out;
+  a.key = scratch_key;
+  const int64_t total = before * len * after;
+  TimedLaunch t("group_stats", st);
+  hipLaunchKernelGGL(group_init_kernel, dim3(grid_for(cells)), dim3(256), 0, st, a);
+  if (total > 0) hipLaunchKernelGGL(group_max_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);
+  if (total > 0) hipLaunchKernelGGL(group_sum_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(group_keys_to_max_kernel, dim3(grid_for(cells)), dim3(256), 0, st, a);
+  return check_launch("ogn_group_stats_atomic");
+}
+
+int ogn_group_softmax_apply(const void* src, int dtype, const void* index, int index_dtype, int64_t before,
+                            int64_t len, int64_t after, int64_t groups, const float* m, const float* s,
+                            void* out, int log_softmax, void* stream) {
+  if (before < 0 || len < 0 || after < 0 || groups < 0)
+    return fail(OGN_EINVAL, "ogn_group_softmax_apply: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_group_softmax_apply: dtype must be float32, float16 or bfloat16");
+  if (index_dtype != OGN_I32 && index_dtype != OGN_I64)
+    return fail(OGN_EINVAL, "ogn_group_softmax_apply: index dtype must be int32 or int64");
+  const int64_t total = before * len * after;
+  if (total == 0) return OGN_OK;
+  if (!src || !index || !out || (groups > 0 && (!m || !s)))
+    return fail(OGN_EINVAL, "ogn_group_softmax_apply: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  GroupArgs a{};
+  a.src = src;
+  a.dt = dtype;
+  a.index = index;
+  a.idx64 = index_dtype == OGN_I64;
+  a.before = before;
+  a.len = len;
+  a.after = after;
+  a.groups = groups;
+  a.m = const_cast<float*>(m);
+  a.s = const_cast<float*>(s);
+  a.out = out;
+  a.mode = log_softmax ? 1 : 0;
+  TimedLaunch t("group_apply", st);
+  hipLaunchKernelGGL(group_apply_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);
+  return check_launch("ogn_group_softmax_apply");
+}
+
+int ogn_group_lse_from_stats(const float* m, const float* s, int64_t cells, void* out, int dtype, void* stream) {
+  if (cells < 0) return fail(OGN_EINVAL, "ogn_group_lse_from_stats: negative size");
+  if (cells == 0) return OGN_OK;
+  if (!m || !s || !out) return fail(OGN_EINVAL, "ogn_group_lse_from_stats: null pointer");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_group_lse_from_stats: dtype must be float32, float16 or bfloat16");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  GroupArgs a{};
+  a.before = 1;
+  a.groups = cells;
+  a.after = 1;
+  a.m = const_cast<float*>(m);
+  a.s = const_cast<float*>(s);
+  a.out = out;
+  a.dt = dtype;
+  TimedLaunch t("group_lse", st);
+  hipLaunchKernelGGL(group_lse_kernel, dim3(grid_for(cells)), dim3(256), 0, st, a);
+  return check_launch("ogn_group_lse_from_stats");
+}
+
+}  // extern "C"

@@ -14,6 +14,16 @@ from ._lib import arch
 from .convert import ind2ptr, ptr2ind
 from . import torch_sparse_spmm
 from .torch_sparse_spmm import csr_spmm, coo_spmm, coo_to_csr
+from .segment import (
+    segment_csr, segment_sum_csr, segment_add_csr, segment_mean_csr, segment_min_csr, segment_max_csr,
+    segment_max_csr_legacy, segment_reduce,
+    segment_coo, segment_sum_coo, segment_add_coo, segment_mean_coo, segment_min_coo, segment_max_coo,
+    segment_logsumexp,
+)
+from .scatter import (
+    scatter, scatter_sum, scatter_add, scatter_mul, scatter_mean, scatter_min, scatter_max,
+)
+from .softmax import scatter_softmax, scatter_log_softmax, scatter_logsumexp
 
 __version__ = "0.1.0"
 
@@ -28,4 +38,10 @@ __all__ = [
     "coo_to_csr",
     "torch_sparse_spmm",
     "native_available",
+    "segment_csr", "segment_sum_csr", "segment_add_csr", "segment_mean_csr", "segment_min_csr",
+    "segment_max_csr", "segment_max_csr_legacy", "segment_reduce",
+    "segment_coo", "segment_sum_coo", "segment_add_coo", "segment_mean_coo", "segment_min_coo",
+    "segment_max_coo", "segment_logsumexp",
+    "scatter", "scatter_sum", "scatter_add", "scatter_mul", "scatter_mean", "scatter_min", "scatter_max",
+    "scatter_softmax", "scatter_log_softmax", "scatter_logsumexp",
 ]

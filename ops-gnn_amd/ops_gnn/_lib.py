@@ -58,7 +58,25 @@ SIGNATURES = {
                             _vp, _int, _vp, _int, _vp, _sz, _vp]),
     "ogn_ind2ptr": (_int, [_vp, _int, _i64, _i64, _vp, _vp]),
     "ogn_ptr2ind": (_int, [_vp, _int, _i64, _i64, _vp, _vp]),
+    "ogn_segment_reduce_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _int, _int]),
+    "ogn_segment_reduce": (_int, [_vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _int,
+                                  _vp, _sz, _vp]),
+    "ogn_ind2ptr_batched": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
+    "ogn_index_facts": (_int, [_vp, _i64, _vp, _vp]),
+    "ogn_segment_group_stats": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "ogn_scatter_atomic_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
+    "ogn_scatter_atomic": (_int, [_vp, _int, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _int,
+                                  _int, _vp, _sz, _vp]),
+    "ogn_group_stats_atomic": (_int, [_vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "ogn_group_softmax_apply": (_int, [_vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _int,
+                                       _vp]),
+    "ogn_group_lse_from_stats": (_int, [_vp, _vp, _i64, _vp, _int, _vp]),
 }
+
+# reduce / semantics codes (include/ogn.h)
+R_SUM, R_MEAN, R_MIN, R_MAX, R_PROD, R_LSE = range(6)
+SEM_SEGMENT_CSR, SEM_SEGMENT_COO, SEM_SCATTER = range(3)
+SEG_HAS_OUT = 1
 
 for _name, (_res, _args) in SIGNATURES.items():
     _fn = getattr(_so, _name)

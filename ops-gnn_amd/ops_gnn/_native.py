@@ -90,3 +90,152 @@ def spmm_forward(ptr: torch.Tensor, col: torch.Tensor, value: Optional[torch.Ten
                           dptr(ws), ws_bytes, stream_of(mat))
     check(rc, "spmm")
     return out, arg
+
+
+# ------------------------------------------------------------------ segment engine
+SEGMENT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def segment_reduce(src3: torch.Tensor, ptr2d: torch.Tensor, segments: int, reduce: int, semantics: int,
+                   out3: Optional[torch.Tensor] = None, has_out: bool = False, need_arg: bool = False
+                   ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Contiguous-segment reduction (include/ogn.h ogn_segment_reduce).
+
+    src3 [B, L, F] contiguous; ptr2d int64 [1 | B, S+1] contiguous; out3
+    [B, S, F] contiguous (holding seeds when has_out).  Returns (out3, arg3).
+    """
+    b, length, f = src3.shape
+    if out3 is None:
+        out3 = torch.empty((b, segments, f), dtype=src3.dtype, device=src3.device)
+    arg = torch.empty((b, segments, f), dtype=torch.int64, device=src3.device) if need_arg else None
+    if out3.numel() == 0:
+        return out3, arg
+    pb = ptr2d.shape[0]
+    code = _lib.TORCH_TO_OGN[src3.dtype]
+    ws_bytes = lib.ogn_segment_reduce_workspace_size(b, length, segments, f, pb, code, reduce)
+    ws = _lib.workspace(ws_bytes, src3.device)
+    rc = lib.ogn_segment_reduce(dptr(ptr2d), pb, dptr(src3), code, b, length, segments, f, dptr(out3), dptr(arg),
+                                reduce, semantics, _lib.SEG_HAS_OUT if has_out else 0, dptr(ws), ws_bytes,
+                                stream_of(src3))
+    check(rc, "segment reduction")
+    return out3, arg
+
+
+def ind2ptr_batched(index2d: torch.Tensor, rows: int) -> torch.Tensor:
+    ib, numel = index2d.shape
+    out = torch.empty((ib, rows + 1), dtype=torch.int64, device=index2d.device)
+    if numel == 0:
+        return out.zero_()
+    index2d = index2d.contiguous()
+    check(lib.ogn_ind2ptr_batched(dptr(index2d), ib, numel, rows, dptr(out), stream_of(index2d)), "ind2ptr")
+    return out
+
+
+class _VersionCache:
+    """Per-tensor facts keyed by identity + version (the reference's proof /
+    bounds caches, e.g. python/ops_gnn/scatter.py:134-178)."""
+
+    def __init__(self, limit=256):
+        from collections import OrderedDict
+        self._d = OrderedDict()
+        self._limit = limit
+
+    def get(self, t, compute):
+        import weakref
+        try:
+            version = t._version
+        except (AttributeError, RuntimeError):
+            return compute()
+        key = (id(t), t.data_ptr(), tuple(t.shape), tuple(t.stride()), version)
+        hit = self._d.get(key)
+        if hit is not None and hit[0]() is t:
+            self._d.move_to_end(key)
+            return hit[1]
+        value = compute()
+        self._d[key] = (weakref.ref(t), value)
+        if len(self._d) > self._limit:
+            self._d.popitem(last=False)
+        return value
+
+    def clear(self):
+        self._d.clear()
+
+
+INDEX_FACTS = _VersionCache()
+
+
+def index_facts(index: torch.Tensor) -> Tuple[bool, int, int]:
+    """(sorted, min, max) of an int64 index; one 24-byte device-to-host read,
+    cached per tensor version."""
+
+    def compute():
+        idx = index.contiguous()
+        facts = torch.empty(3, dtype=torch.int64, device=idx.device)
+        check(lib.ogn_index_facts(dptr(idx), idx.numel(), dptr(facts), stream_of(idx)), "index facts")
+        unsorted, mn, mx = facts.tolist()
+        return (unsorted == 0, mn, mx)
+
+    return INDEX_FACTS.get(index, compute)
+
+
+def scatter_atomic(src3: torch.Tensor, index: torch.Tensor, strides, size: int, reduce: int,
+                   out3: torch.Tensor, has_out: bool) -> Optional[torch.Tensor]:
+    """Unsorted scatter into out3 [B, size, F] (modified in place); returns arg."""
+    b, length, f = src3.shape
+    need_arg = reduce in (_lib.R_MIN, _lib.R_MAX)
+    arg = torch.empty((b, size, f), dtype=torch.int64, device=src3.device) if need_arg else None
+    if out3.numel() == 0:
+        return arg
+    ws_bytes = lib.ogn_scatter_atomic_workspace_size(b, size, f, reduce)
+    ws = _lib.workspace(ws_bytes, src3.device)
+    rc = lib.ogn_scatter_atomic(dptr(src3), _lib.TORCH_TO_OGN[src3.dtype], dptr(index), strides[0], strides[1],
+                                strides[2], b, length, f, size, dptr(out3), dptr(arg), reduce, 1 if has_out else 0,
+                                dptr(ws), ws_bytes, stream_of(src3))
+    check(rc, "scatter")
+    return arg
+
+
+def group_stats(src3: torch.Tensor, index: torch.Tensor, groups: int, sorted_index: bool
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-(batch, group, feature) max and sum(exp(x - clamp(max))), fp32."""
+    b, length, f = src3.shape
+    m = torch.empty((b, groups, f), dtype=torch.float32, device=src3.device)
+    s = torch.empty_like(m)
+    if m.numel() == 0:
+        return m, s
+    code = _lib.TORCH_TO_OGN[src3.dtype]
+    if sorted_index:
+        ptr = ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups)
+        ws_bytes = lib.ogn_segment_reduce_workspace_size(b, length, groups, f, 1, code, _lib.R_LSE)
+        ws = _lib.workspace(ws_bytes, src3.device)
+        rc = lib.ogn_segment_group_stats(dptr(ptr), dptr(src3), code, b, length, groups, f, dptr(m), dptr(s),
+                                         dptr(ws), ws_bytes, stream_of(src3))
+    else:
+        idx = index.contiguous()
+        key = torch.empty(m.shape, dtype=torch.int32, device=src3.device)
+        rc = lib.ogn_group_stats_atomic(dptr(src3), code, dptr(idx), _index_code(idx), b, length, f, groups,
+                                        dptr(m), dptr(s), dptr(key), stream_of(src3))
+    check(rc, "group statistics")
+    return m, s
+
+
+def group_softmax_apply(src3, index, groups, m, s, log_softmax: bool) -> torch.Tensor:
+    b, length, f = src3.shape
+    out = torch.empty_like(src3)
+    if out.numel() == 0:
+        return out
+    idx = index.contiguous()
+    rc = lib.ogn_group_softmax_apply(dptr(src3), _lib.TORCH_TO_OGN[src3.dtype], dptr(idx), _index_code(idx), b,
+                                     length, f, groups, dptr(m), dptr(s), dptr(out), 1 if log_softmax else 0,
+                                     stream_of(src3))
+    check(rc, "group softmax")
+    return out
+
+
+def group_lse_from_stats(m, s, dtype) -> torch.Tensor:
+    out = torch.empty(m.shape, dtype=dtype, device=m.device)
+    if out.numel() == 0:
+        return out
+    check(lib.ogn_group_lse_from_stats(dptr(m), dptr(s), m.numel(), dptr(out), _lib.TORCH_TO_OGN[dtype],
+                                       stream_of(m)), "group logsumexp")
+    return out

@@ -1,0 +1,143 @@
+"""torch_scatter-compatible scatter family on the GPU.
+
+Public API and rules of the reference python/ops_gnn/scatter.py:555-674
+(torch_scatter 2.1.2 semantics with the Ascend 950 "later writer wins" tie
+rule for min/max): index broadcast (`broadcast`), negative dims, `out`
+updated in place (identity preserved), dim_size inferred from the index,
+positions never written by min/max get arg = src.size(dim) and value 0 when
+`out` is omitted.
+
+Two execution paths, both HIP:
+  * sorted 1-D index along `dim` (the common message-passing layout) -> the
+    deterministic contiguous-segment engine (include/ogn.h ogn_segment_reduce
+    with OGN_SEM_SCATTER);
+  * any other index -> the atomic scatter (ogn_scatter_atomic).
+Index sortedness and bounds come from one cached device probe per index
+version.  float32 / float16 / bfloat16 only; other dtypes raise TypeError.
+"""
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib, _native
+from ._native import SEGMENT_DTYPES
+
+_REDUCE_CODE = {"sum": _lib.R_SUM, "add": _lib.R_SUM, "mul": _lib.R_PROD, "mean": _lib.R_MEAN,
+                "min": _lib.R_MIN, "max": _lib.R_MAX}
+
+
+def native_available() -> bool:
+    return True
+
+
+def broadcast(src: torch.Tensor, other: torch.Tensor, dim: int) -> torch.Tensor:
+    """Broadcast ``src`` to ``other`` with torch_scatter's index rules."""
+    if dim < 0:
+        dim = other.dim() + dim
+    if src.dim() == 1:
+        for _ in range(0, dim):
+            src = src.unsqueeze(0)
+    for _ in range(src.dim(), other.dim()):
+        src = src.unsqueeze(-1)
+    return src.expand(other.size())
+
+
+def _normalize_dim(src: torch.Tensor, dim: int) -> int:
+    if not isinstance(dim, int) or isinstance(dim, bool):
+        raise TypeError("dim must be an int")
+    if src.dim() < 1 or src.dim() > 8:
+        raise ValueError("src must have between 1 and 8 dimensions")
+    if dim < -src.dim() or dim >= src.dim():
+        raise IndexError(f"Dimension out of range (expected to be in range of [-{src.dim()}, {src.dim() - 1}], "
+                         f"but got {dim})")
+    return dim + src.dim() if dim < 0 else dim
+
+
+def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Optional[torch.Tensor],
+                     dim_size: Optional[int], reduce: str) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    if reduce not in _REDUCE_CODE:
+        raise ValueError("reduce must be one of 'sum', 'add', 'mul', 'mean', 'min', or 'max'")
+    dim = _normalize_dim(src, dim)
+    if index.dtype != torch.int64:
+        raise TypeError(f"index must have dtype torch.int64, got {index.dtype}")
+    if src.dtype not in SEGMENT_DTYPES:
+        raise TypeError(f"scatter: unsupported dtype {src.dtype} (float32, float16 and bfloat16 run on the GPU)")
+    _lib.require_gpu(src, index, what="scatter")
+    expanded = broadcast(index, src, dim)
+    compact = index.dim() == 1 and index.numel() == src.size(dim)
+    if out is not None:
+        size = out.size(dim)
+    elif dim_size is not None:
+        size = int(dim_size)
+    else:
+        size = (_native.index_facts(index)[2] + 1) if index.numel() else 0
+    shape = list(src.shape)
+    shape[dim] = size
+    if out is not None:
+        if out.dtype != src.dtype or list(out.shape) != shape or out.device != src.device:
+            raise ValueError("out must match src's dtype and device and have the scatter output shape")
+    before, length, after = math.prod(src.shape[:dim]), src.size(dim), math.prod(src.shape[dim + 1:])
+    code = _REDUCE_CODE[reduce]
+    has_out = out is not None
+    is_minmax = reduce in ("min", "max")
+    if has_out:
+        out3 = out.view(before, size, after) if out.is_contiguous() else out.contiguous().view(before, size, after)
+    else:
+        out3 = torch.empty((before, size, after), dtype=src.dtype, device=src.device)
+    if out3.numel() == 0:
+        arg = torch.full(shape, length, dtype=torch.int64, device=src.device) if is_minmax else None
+        return (out if has_out else out3.reshape(shape)), arg
+    src3 = src.contiguous().reshape(before, length, after)
+    arg3 = None
+    use_segments = False
+    if compact and index.numel() > 0:
+        is_sorted, mn, mx = _native.index_facts(index)
+        use_segments = is_sorted and mn >= 0 and mx < size
+    if use_segments:
+        ptr = _native.ind2ptr_batched(index.reshape(1, -1), size)
+        res3, arg3 = _native.segment_reduce(src3, ptr, size, code, _lib.SEM_SCATTER, out3, has_out, is_minmax)
+    else:
+        if compact:
+            idx, strides = index.contiguous(), (0, 1, 0)
+        else:
+            idx, strides = expanded.contiguous(), (length * after, after, 1)
+        arg3 = _native.scatter_atomic(src3, idx, strides, size, code, out3, has_out)
+        res3 = out3
+    result = res3.reshape(shape)
+    if has_out and result.data_ptr() != out.data_ptr():
+        out.copy_(result)
+        result = out
+    elif has_out:
+        result = out
+    return result, (None if arg3 is None else arg3.reshape(shape))
+
+
+def scatter_sum(src, index, dim: int = -1, out=None, dim_size=None) -> torch.Tensor:
+    return _scatter_forward(src, index, dim, out, dim_size, "sum")[0]
+
+
+def scatter_add(src, index, dim: int = -1, out=None, dim_size=None) -> torch.Tensor:
+    return scatter_sum(src, index, dim, out, dim_size)
+
+
+def scatter_mul(src, index, dim: int = -1, out=None, dim_size=None) -> torch.Tensor:
+    return _scatter_forward(src, index, dim, out, dim_size, "mul")[0]
+
+
+def scatter_mean(src, index, dim: int = -1, out=None, dim_size=None) -> torch.Tensor:
+    return _scatter_forward(src, index, dim, out, dim_size, "mean")[0]
+
+
+def scatter_min(src, index, dim: int = -1, out=None, dim_size=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _scatter_forward(src, index, dim, out, dim_size, "min")
+
+
+def scatter_max(src, index, dim: int = -1, out=None, dim_size=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _scatter_forward(src, index, dim, out, dim_size, "max")
+
+
+def scatter(src, index, dim: int = -1, out=None, dim_size=None, reduce: str = "sum") -> torch.Tensor:
+    """``torch_scatter.scatter(src, index, dim, out, dim_size, reduce)``."""
+    return _scatter_forward(src, index, dim, out, dim_size, reduce)[0]

@@ -1,0 +1,312 @@
+"""segment_csr / segment_coo / segment_reduce / segment_logsumexp on the GPU.
+
+Public names, signatures and return conventions follow the reference
+(python/ops_gnn/segment_csr.py:35-91, segment_reduce.py:32-66,
+segment_coo.py:33-128, segment_logsumexp.py:108-155,
+segment_max_csr.py:19-50).  Every reduction runs on the contiguous-segment
+CSR engine (include/ogn.h ogn_segment_reduce): deterministic, one writer per
+output, nnz-balanced across wavefronts.  Supported dtypes: float32, float16,
+bfloat16 (fp32 arithmetic); other dtypes raise TypeError -- there is no CPU
+fallback.
+"""
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib, _native
+from ._native import SEGMENT_DTYPES
+
+_REDUCE_OPS = ("sum", "add", "mean", "min", "max")
+_CODE = {"sum": _lib.R_SUM, "add": _lib.R_SUM, "mean": _lib.R_MEAN, "min": _lib.R_MIN, "max": _lib.R_MAX}
+
+_PTR_FACTS = _native._VersionCache()
+
+
+def _check_reduce(reduce: str) -> None:
+    if reduce not in _REDUCE_OPS:
+        raise ValueError(f"reduce value '{reduce}' is not valid (use one of {_REDUCE_OPS})")
+
+
+def _check_dtype(src: torch.Tensor, op: str) -> None:
+    if src.dtype not in SEGMENT_DTYPES:
+        raise TypeError(f"{op}: unsupported dtype {src.dtype} (float32, float16 and bfloat16 run on the GPU)")
+
+
+def _split(shape, dim):
+    return math.prod(shape[:dim]), shape[dim], math.prod(shape[dim + 1:])
+
+
+def _pointer_ok(ptr2d: torch.Tensor, length: int) -> bool:
+    """Non-decreasing and inside [0, length] (one 4-byte device-to-host read,
+    cached per tensor version)."""
+    def compute():
+        p = ptr2d
+        bad = (p < 0).any() | (p > length).any()
+        if p.size(-1) > 1:
+            bad = bad | (p[..., 1:] < p[..., :-1]).any()
+        return not bool(bad.item())
+    return _PTR_FACTS.get(ptr2d, compute)
+
+
+def _prepare_out(out, shape, src, op):
+    if out is None:
+        return None
+    if not isinstance(out, torch.Tensor):
+        raise TypeError(f"{op}: out must be a torch.Tensor")
+    if out.dtype != src.dtype:
+        raise RuntimeError(f"out dtype ({out.dtype}) must match src ({src.dtype})")
+    if tuple(out.shape) != tuple(shape):
+        raise RuntimeError(f"out shape {tuple(out.shape)} must be {tuple(shape)}")
+    if out.device != src.device:
+        raise RuntimeError("out must live on src's device")
+    return out
+
+
+def _finish(result3, out, shape):
+    result = result3.reshape(shape)
+    if out is None:
+        return result
+    if result.data_ptr() != out.data_ptr():
+        out.copy_(result)
+    return out
+
+
+# ------------------------------------------------------------------ segment_csr
+def _segment_csr(src, indptr, out, reduce, return_arg):
+    _lib.require_gpu(src, indptr, what="segment_csr")
+    if indptr.dtype != torch.int64:
+        raise RuntimeError(f"indptr must be int64, got {indptr.dtype}")
+    if indptr.dim() < 1:
+        raise RuntimeError("indptr must have at least 1 dim")
+    if src.dim() < indptr.dim():
+        raise RuntimeError(f"src.dim() ({src.dim()}) must be >= indptr.dim() ({indptr.dim()})")
+    if indptr.size(-1) < 1:
+        raise RuntimeError("indptr last dim must be >= 1")
+    dim = indptr.dim() - 1
+    for i in range(dim):
+        if indptr.size(i) not in (1, src.size(i)):
+            raise RuntimeError(f"indptr leading dim {i} ({indptr.size(i)}) must be 1 or src.size({i}) "
+                               f"({src.size(i)})")
+    _check_dtype(src, "segment_csr")
+    segs = indptr.size(-1) - 1
+    before, length, after = _split(src.shape, dim)
+    shape = list(src.shape)
+    shape[dim] = segs
+    out = _prepare_out(out, shape, src, "segment_csr")
+    if src.numel() == 0 or segs == 0:
+        if out is not None:
+            res = out
+        else:
+            res = torch.zeros(shape, dtype=src.dtype, device=src.device)
+        arg = torch.full(shape, length, dtype=torch.int64, device=src.device)
+        return res, arg
+    if all(indptr.size(i) == 1 for i in range(dim)):
+        ptr2d = indptr.reshape(1, -1).contiguous()
+    else:
+        ptr2d = indptr.expand(*src.shape[:dim], segs + 1).reshape(before, segs + 1).contiguous()
+    if not _pointer_ok(ptr2d, length):
+        raise RuntimeError("indptr must be nondecreasing and within [0, src.size(dim)]")
+    src3 = src.contiguous().reshape(before, length, after)
+    direct = out is not None and out.is_contiguous()
+    out3 = out.view(before, segs, after) if direct else None
+    res3, arg3 = _native.segment_reduce(src3, ptr2d, segs, _CODE[reduce], _lib.SEM_SEGMENT_CSR, out3,
+                                        False, return_arg and reduce in ("min", "max"))
+    result = _finish(res3, out, shape)
+    return result, (None if arg3 is None else arg3.reshape(shape))
+
+
+def segment_sum_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return _segment_csr(src, indptr, out, "sum", False)[0]
+
+
+def segment_add_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return _segment_csr(src, indptr, out, "add", False)[0]
+
+
+def segment_mean_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return _segment_csr(src, indptr, out, "mean", False)[0]
+
+
+def segment_min_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _segment_csr(src, indptr, out, "min", True)
+
+
+def segment_max_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Values and first indices of the segment maxima.
+
+    An int32 indptr selects the legacy value-only entry (segment_max_csr_legacy),
+    as in the reference (python/ops_gnn/segment_csr.py:64-77).
+    """
+    if isinstance(indptr, torch.Tensor) and indptr.dtype == torch.int32:
+        return segment_max_csr_legacy(src, indptr, out)
+    return _segment_csr(src, indptr, out, "max", True)
+
+
+def segment_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None,
+                reduce: str = "sum") -> torch.Tensor:
+    """Reduce CSR segments along ``indptr.dim() - 1``; values only."""
+    _check_reduce(reduce)
+    return _segment_csr(src, indptr, out, reduce, False)[0]
+
+
+def segment_reduce(src: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None,
+                   reduce: str = "sum") -> torch.Tensor:
+    """DGL ``segment_reduce``: promote int32 offsets to int64 and call segment_csr."""
+    if offsets.dtype != torch.int64:
+        offsets = offsets.to(torch.int64)
+    return segment_csr(src, offsets, out, reduce)
+
+
+def segment_max_csr_legacy(src: torch.Tensor, indptr: torch.Tensor, optional_out: Optional[torch.Tensor] = None):
+    """Legacy value-only segment max (reference python/ops_gnn/segment_max_csr.py:19-50,
+    golden test/segment_max_csr/arch35/golden.py:16-41): empty segments give 0;
+    a non-empty ``optional_out`` seeds the result as max(segment max, optional_out)."""
+    ptr = indptr.to(torch.int64)
+    values, _ = _segment_csr(src, ptr, None, "max", False)
+    if optional_out is not None and optional_out.numel() > 0:
+        if optional_out.shape != values.shape:
+            raise RuntimeError("optional_out must have the output shape")
+        values = torch.maximum(values, optional_out.to(values.dtype))
+    return values
+
+
+# ------------------------------------------------------------------ segment_coo
+def _segment_coo(src, index, out, dim_size, reduce, return_arg):
+    _lib.require_gpu(src, index, what="segment_coo")
+    if index.dtype != torch.int64:
+        raise ValueError("indices must be an int64 tensor with valid rank")
+    if index.dim() < 1 or index.dim() > src.dim():
+        raise ValueError("indices must be an int64 tensor with valid rank")
+    if reduce not in _CODE:
+        raise ValueError("segment_coo supports sum/add/mean/min/max, not " + str(reduce))
+    _check_dtype(src, "segment_coo")
+    dim = index.dim() - 1
+    for i in range(dim + 1):
+        if index.size(i) not in (1, src.size(i)) or (i == dim and index.size(i) != src.size(i)):
+            raise ValueError("index shape must broadcast to src")
+    before, length, after = _split(src.shape, dim)
+    if out is not None:
+        segs = out.size(dim)
+    elif dim_size is not None:
+        segs = int(dim_size)
+    else:
+        segs = (_native.index_facts(index)[2] + 1) if index.numel() else 0
+    shape = list(src.shape)
+    shape[dim] = segs
+    out = _prepare_out(out, shape, src, "segment_coo")
+    if all(index.size(i) == 1 for i in range(dim)):
+        idx2d = index.reshape(1, -1)
+    else:
+        idx2d = index.expand(*src.shape[:dim], length).reshape(before, length)
+    if src.numel() == 0 or segs == 0:
+        res = out if out is not None else torch.zeros(shape, dtype=src.dtype, device=src.device)
+        return res, torch.full(shape, length, dtype=torch.int64, device=src.device)
+    ptr2d = _native.ind2ptr_batched(idx2d.contiguous(), segs)
+    src3 = src.contiguous().reshape(before, length, after)
+    has_out = out is not None
+    direct = has_out and out.is_contiguous()
+    if has_out:
+        out3 = out.view(before, segs, after) if direct else out.contiguous().reshape(before, segs, after)
+    else:
+        out3 = None
+    res3, arg3 = _native.segment_reduce(src3, ptr2d, segs, _CODE[reduce], _lib.SEM_SEGMENT_COO, out3, has_out,
+                                        return_arg and reduce in ("min", "max"))
+    result = _finish(res3, out, shape)
+    return result, (None if arg3 is None else arg3.reshape(shape))
+
+
+def segment_sum_coo(src, index, out=None, dim_size=None) -> torch.Tensor:
+    """Sum segments of a sorted index (a supplied out is overwritten, Ascend 950 rule)."""
+    return _segment_coo(src, index, out, dim_size, "sum", False)[0]
+
+
+def segment_add_coo(src, index, out=None, dim_size=None) -> torch.Tensor:
+    return segment_sum_coo(src, index, out, dim_size)
+
+
+def segment_mean_coo(src, index, out=None, dim_size=None) -> torch.Tensor:
+    """Segment means; a supplied out seeds the numerator."""
+    return _segment_coo(src, index, out, dim_size, "mean", False)[0]
+
+
+def segment_min_coo(src, index, out=None, dim_size=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Minima and int64 positions; later ties win (Ascend 950 convention)."""
+    return _segment_coo(src, index, out, dim_size, "min", True)
+
+
+def segment_max_coo(src, index, out=None, dim_size=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _segment_coo(src, index, out, dim_size, "max", True)
+
+
+def segment_coo(src, index, out=None, dim_size=None, reduce: str = "sum") -> torch.Tensor:
+    """Reduce along ``index.dim() - 1`` over a sorted int64 index; values only."""
+    if reduce not in _CODE:
+        raise ValueError("segment_coo supports sum/add/mean/min/max, not " + str(reduce))
+    return _segment_coo(src, index, out, dim_size, reduce, False)[0]
+
+
+# ------------------------------------------------------------------ segment_logsumexp
+_MAX_POINTER = 2 ** 31 - 1
+
+
+def segment_logsumexp(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """log(sum(exp(src))) over CSR segments along dim 0 (fp32 math, shift
+    clamped to +-FLT_MAX; empty segments give -inf).  Argument checks and
+    messages follow the reference (python/ops_gnn/segment_logsumexp.py:44-105)."""
+    if not isinstance(src, torch.Tensor):
+        raise TypeError(f"src must be a torch.Tensor, got {type(src).__name__}")
+    if not isinstance(indptr, torch.Tensor):
+        raise TypeError(f"indptr must be a torch.Tensor, got {type(indptr).__name__}")
+    if src.dim() < 1:
+        raise ValueError("src must have at least one dimension")
+    if indptr.dim() != 1:
+        raise ValueError(f"indptr must be 1-D, got {indptr.dim()}-D")
+    if src.dtype not in SEGMENT_DTYPES:
+        raise TypeError(f"src dtype must be one of float16, float32, bfloat16; got {src.dtype}")
+    if indptr.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"indptr dtype must be int32 or int64, got {indptr.dtype}")
+    if src.device != indptr.device:
+        raise ValueError(f"src and indptr must be on the same device, got {src.device} and {indptr.device}")
+    _lib.require_gpu(src, what="segment_logsumexp")
+    if indptr.numel() < 1:
+        raise ValueError("indptr must contain at least one boundary")
+    ptr = indptr.to(torch.int64).contiguous()
+    flags = torch.stack(((ptr < 0).any().to(torch.int64), (ptr[1:] < ptr[:-1]).any().to(torch.int64),
+                         ptr[-1])).cpu()
+    if int(flags[0]):
+        raise ValueError("indptr must be non-negative")
+    if int(flags[1]):
+        raise ValueError("indptr must be nondecreasing")
+    if int(flags[2]) != src.size(0):
+        raise ValueError(f"indptr[-1] ({int(flags[2])}) must equal src.size(0) ({src.size(0)})")
+    if src.size(0) > _MAX_POINTER:
+        raise ValueError(f"src.size(0) must fit the int32 pointer range, got {src.size(0)}")
+    segs = ptr.numel() - 1
+    shape = (segs,) + tuple(src.shape[1:])
+    if out is not None:
+        if not isinstance(out, torch.Tensor):
+            raise TypeError(f"out must be a torch.Tensor, got {type(out).__name__}")
+        if tuple(out.shape) != shape:
+            raise ValueError(f"out shape must be {shape}, got {tuple(out.shape)}")
+        if out.dtype != src.dtype:
+            raise TypeError(f"out dtype must match src ({src.dtype}), got {out.dtype}")
+        if out.device != src.device:
+            raise ValueError(f"out device must match src ({src.device}), got {out.device}")
+    if segs == 0:
+        result = torch.empty(shape, dtype=src.dtype, device=src.device)
+    elif src.numel() == 0:
+        result = torch.full(shape, float("-inf"), dtype=src.dtype, device=src.device)
+    else:
+        length = src.size(0)
+        after = math.prod(src.shape[1:])
+        res3, _ = _native.segment_reduce(src.contiguous().reshape(1, length, after), ptr.reshape(1, -1), segs,
+                                         _lib.R_LSE, _lib.SEM_SEGMENT_CSR)
+        result = res3.reshape(shape)
+    if out is not None:
+        out.copy_(result)
+        return out
+    return result

@@ -1,0 +1,128 @@
+"""Grouped softmax family: scatter_softmax, scatter_log_softmax, scatter_logsumexp.
+
+Argument handling and error contract of the reference
+(python/ops_gnn/_grouped_softmax.py:33-155, scatter_softmax.py:46-75,
+scatter_log_softmax.py:49-79, scatter_logsumexp.py:86-127): `index` is a
+1-D int32/int64 vector along `dim` (length src.size(dim)), groups =
+`dim_size` (default index.max() + 1), every index value must lie in
+[0, dim_size).
+
+Forward, all HIP: per-(batch, group, feature) statistics m = max and
+s = sum(exp(x - clamp(m))) -- from the contiguous-segment engine when the
+index is sorted (deterministic), from atomics otherwise -- then one
+elementwise pass (softmax / log_softmax) or one pass over the groups
+(logsumexp).  fp32 math for every dtype.
+"""
+
+from typing import Optional
+
+import math
+import torch
+
+from . import _lib, _native
+
+SUPPORTED_DTYPES = (torch.float16, torch.float32, torch.bfloat16)
+SUPPORTED_INDEX_DTYPES = (torch.int32, torch.int64)
+
+
+def normalize_dim(dim: int, rank: int) -> int:
+    if not isinstance(dim, int) or isinstance(dim, bool):
+        raise TypeError(f"dim must be an int, got {type(dim).__name__}")
+    if dim < -rank or dim >= rank:
+        raise IndexError(f"Dimension out of range (expected to be in range of [-{rank}, {rank - 1}], but got {dim})")
+    return dim + rank if dim < 0 else dim
+
+
+def check_inputs(op: str, src: torch.Tensor, index: torch.Tensor, dim: int) -> None:
+    if src.dim() < 1:
+        raise ValueError("src must have at least one dimension")
+    if index.dim() != 1:
+        raise ValueError(f"index must be 1-D, got {index.dim()}-D")
+    if src.dtype not in SUPPORTED_DTYPES:
+        raise TypeError(f"src dtype must be one of float16, float32, bfloat16; got {src.dtype}")
+    if index.dtype not in SUPPORTED_INDEX_DTYPES:
+        raise TypeError(f"index dtype must be int32 or int64, got {index.dtype}")
+    if src.device != index.device:
+        raise ValueError(f"src and index must be on the same device, got {src.device} and {index.device}")
+    if src.device.type != "cuda":
+        raise RuntimeError(f"{op} requires GPU tensors")
+    if index.numel() != src.size(dim):
+        raise ValueError(f"index length ({index.numel()}) must match src.size({dim}) ({src.size(dim)})")
+
+
+def resolve_dim_size(index: torch.Tensor, dim_size: Optional[int], facts) -> int:
+    if dim_size is None:
+        return facts[2] + 1 if index.numel() > 0 else 0
+    if not isinstance(dim_size, int) or isinstance(dim_size, bool):
+        raise TypeError(f"dim_size must be an int, got {type(dim_size).__name__}")
+    if dim_size < 0:
+        raise ValueError(f"dim_size must be non-negative, got {dim_size}")
+    if dim_size > 2 ** 31 - 1:
+        raise ValueError(f"dim_size must fit the int32 index range, got {dim_size}")
+    return dim_size
+
+
+def _facts(index: torch.Tensor):
+    if index.numel() == 0:
+        return (True, 0, -1)
+    return _native.index_facts(index.to(torch.int64) if index.dtype != torch.int64 else index)
+
+
+def _prepare(op, src, index, dim, dim_size):
+    if not isinstance(src, torch.Tensor):
+        raise TypeError(f"src must be a torch.Tensor, got {type(src).__name__}")
+    if not isinstance(index, torch.Tensor):
+        raise TypeError(f"index must be a torch.Tensor, got {type(index).__name__}")
+    dim = normalize_dim(dim, src.dim())
+    check_inputs(op, src, index, dim)
+    facts = _facts(index)
+    groups = resolve_dim_size(index, dim_size, facts)
+    if index.numel():
+        if facts[1] < 0:
+            raise ValueError("index must be non-negative")
+        if facts[2] >= groups:
+            raise ValueError(f"index values must be smaller than dim_size ({groups})")
+    before, length, after = math.prod(src.shape[:dim]), src.size(dim), math.prod(src.shape[dim + 1:])
+    src3 = src.contiguous().reshape(before, length, after)
+    return dim, groups, facts[0], src3
+
+
+def _stats(src3, index, groups, is_sorted):
+    return _native.group_stats(src3, index, groups, is_sorted)
+
+
+def scatter_softmax(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
+                    dim_size: Optional[int] = None) -> torch.Tensor:
+    """Softmax over the groups of ``src`` along ``dim`` defined by ``index``."""
+    dim, groups, is_sorted, src3 = _prepare("scatter_softmax", src, index, dim, dim_size)
+    if src.numel() == 0:
+        return torch.zeros_like(src)
+    m, s = _stats(src3, index, groups, is_sorted)
+    return _native.group_softmax_apply(src3, index, groups, m, s, False).reshape(src.shape)
+
+
+def scatter_log_softmax(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
+                        dim_size: Optional[int] = None) -> torch.Tensor:
+    """Log-softmax over the groups of ``src`` along ``dim`` defined by ``index``."""
+    dim, groups, is_sorted, src3 = _prepare("scatter_log_softmax", src, index, dim, dim_size)
+    if src.numel() == 0:
+        return torch.zeros_like(src)
+    m, s = _stats(src3, index, groups, is_sorted)
+    return _native.group_softmax_apply(src3, index, groups, m, s, True).reshape(src.shape)
+
+
+def scatter_logsumexp(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
+                      dim_size: Optional[int] = None) -> torch.Tensor:
+    """log(sum(exp(src))) per group; src.size(dim) is replaced by dim_size,
+    empty groups give -inf."""
+    dim, groups, is_sorted, src3 = _prepare("scatter_logsumexp", src, index, dim, dim_size)
+    shape = list(src.shape)
+    shape[dim] = groups
+    if src3.numel() == 0 or groups == 0:
+        return torch.full(shape, float("-inf"), dtype=src.dtype, device=src.device)
+    if is_sorted:
+        ptr = _native.ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups)
+        res3, _ = _native.segment_reduce(src3, ptr, groups, _lib.R_LSE, _lib.SEM_SEGMENT_CSR)
+        return res3.reshape(shape)
+    m, s = _stats(src3, index, groups, False)
+    return _native.group_lse_from_stats(m, s, src.dtype).reshape(shape)

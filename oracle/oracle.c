@@ -16,6 +16,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define ORACLE_NONE INT64_MAX
@@ -145,4 +146,214 @@ void oracle_segment_csr(const float* src, const int64_t* ptr, int64_t ptr_stride
       }
     }
   }
+}
+
+/* ---------------------------------------------------------------- segment_coo (Ascend 950 rules)
+ * reference csrc/npu/segment_coo/op_kernel/arch35/segment_coo.cpp:114-153
+ * (ReduceSegments), restated as an in-order fold over the sorted index:
+ * src [batch, len, feat]; index [ib, len] (ib = 1 broadcasts); out/arg
+ * [batch, segs, feat].  has_out: `out` holds the caller's values on entry.
+ *  sum: overwrite (start 0).  mean: start from out if has_out, divide by the
+ *  count when non-empty (empty keeps the start value).  min/max: start from
+ *  out (arg = len) if has_out, else from the segment's first element; take
+ *  x when x <= v (min) / x >= v (max), so the LAST extremum wins and NaN
+ *  never enters (a NaN start value stays).  Empty: value 0 (no out) / arg len.
+ */
+void oracle_segment_coo(const float* src, const int64_t* index, int64_t ib, int64_t batch,
+                        int64_t len, int64_t feat, int64_t segs, int reduce, int has_out,
+                        double* out, int64_t* arg) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t* idx = index + (ib == 1 ? 0 : b * len);
+    double* o = out + b * segs * feat;
+    int64_t* ag = arg ? arg + b * segs * feat : 0;
+    for (int64_t i = 0; i < segs * feat; ++i) {
+      if (reduce == 0 || !has_out) o[i] = 0.0; /* sum always overwrites */
+      if (ag) ag[i] = len;
+    }
+    int64_t j = 0;
+    while (j < len) {
+      const int64_t s = idx[j];
+      int64_t z = j;
+      while (z < len && idx[z] == s) ++z;
+      if (s >= 0 && s < segs) {
+        for (int64_t f = 0; f < feat; ++f) {
+          double v;
+          int64_t where = len;
+          int64_t start = j;
+          if (reduce <= 1) {
+            v = (reduce == 1 && has_out) ? o[s * feat + f] : 0.0;
+          } else if (has_out) {
+            v = o[s * feat + f];
+          } else {
+            v = (double)src[(b * len + j) * feat + f];
+            where = j;
+            start = j + 1;
+          }
+          for (int64_t t = (reduce <= 1 ? j : start); t < z; ++t) {
+            const double x = (double)src[(b * len + t) * feat + f];
+            if (reduce <= 1) v += x;
+            else if (reduce == 2 ? x <= v : x >= v) {
+              v = x;
+              where = t;
+            }
+          }
+          if (reduce == 1) v /= (double)(z - j);
+          o[s * feat + f] = v;
+          if (ag && reduce >= 2) ag[s * feat + f] = where;
+        }
+      }
+      j = z;
+    }
+  }
+}
+
+/* ---------------------------------------------------------------- scatter (torch_scatter)
+ * reference test/scatter/arch35/golden.py:35-127: an in-order fold over every
+ * element of src [before, len, after] into out [before, size, after] at
+ * index (same shape as src, already broadcast).  sum/mean add, prod
+ * multiplies; min/max take x when x <= out / x >= out (later tie); mean
+ * divides by the count where the count is non-zero.  Without has_out, out
+ * starts at 0 (sum/mean), 1 (prod) or the dtype's finite extreme `limit`
+ * (min/max), and positions never taken by min/max become 0.  arg = len when
+ * nothing was taken.  reduce codes: 0 sum 1 mean 2 min 3 max 4 prod.
+ */
+void oracle_scatter(const float* src, const int64_t* index, int64_t before, int64_t len, int64_t after,
+                    int64_t size, int reduce, int has_out, double limit, double* out, int64_t* arg) {
+  const int64_t total = before * size * after;
+  int64_t* count = 0;
+  if (reduce == 1) {
+    count = (int64_t*)calloc((size_t)total, sizeof(int64_t));
+  }
+  for (int64_t i = 0; i < total; ++i) {
+    if (!has_out) out[i] = reduce == 4 ? 1.0 : reduce == 2 ? limit : reduce == 3 ? -limit : 0.0;
+    if (arg) arg[i] = len;
+  }
+  for (int64_t b = 0; b < before; ++b)
+    for (int64_t l = 0; l < len; ++l)
+      for (int64_t f = 0; f < after; ++f) {
+        const int64_t t = index[(b * len + l) * after + f];
+        if (t < 0 || t >= size) continue;
+        const double x = (double)src[(b * len + l) * after + f];
+        const int64_t key = (b * size + t) * after + f;
+        if (reduce == 0 || reduce == 1) {
+          out[key] += x;
+          if (count) count[key] += 1;
+        } else if (reduce == 4) {
+          out[key] *= x;
+        } else if (reduce == 2 ? x <= out[key] : x >= out[key]) {
+          out[key] = x;
+          if (arg) arg[key] = l;
+        }
+      }
+  if (count) {
+    for (int64_t i = 0; i < total; ++i)
+      if (count[i] > 0) out[i] /= (double)count[i];
+    free(count);
+  }
+  if (!has_out && (reduce == 2 || reduce == 3) && arg) {
+    for (int64_t i = 0; i < total; ++i)
+      if (arg[i] == len) out[i] = 0.0;
+  }
+}
+
+/* ---------------------------------------------------------------- log-sum-exp
+ * reference test/segment_logsumexp/golden.py:25-44 (torch.logsumexp in
+ * float64 per CSR segment; empty -> -inf).  torch.logsumexp returns NaN if a
+ * NaN is present, +inf if +inf is present, -inf if every term is -inf.
+ */
+static double lse_of(const float* x, int64_t n, int64_t stride) {
+  if (n <= 0) return -INFINITY;
+  double m = -INFINITY;
+  for (int64_t i = 0; i < n; ++i) {
+    const double v = (double)x[i * stride];
+    if (isnan(v)) return NAN;
+    if (v > m) m = v;
+  }
+  if (isinf(m)) return m;
+  double s = 0.0;
+  for (int64_t i = 0; i < n; ++i) s += exp((double)x[i * stride] - m);
+  return m + log(s);
+}
+
+void oracle_segment_lse(const float* src, const int64_t* ptr, int64_t ptr_stride, int64_t batch,
+                        int64_t len, int64_t feat, int64_t segs, double* out) {
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t* p = ptr + b * ptr_stride;
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int64_t s = 0; s < segs; ++s) {
+      int64_t a = p[s], z = p[s + 1];
+      if (z > len) z = len;
+      for (int64_t f = 0; f < feat; ++f)
+        out[(b * segs + s) * feat + f] = a < z ? lse_of(src + (b * len + a) * feat + f, z - a, feat) : -INFINITY;
+    }
+  }
+}
+
+/* ---------------------------------------------------------------- grouped softmax family
+ * reference test/common/grouped_softmax_golden.py:31-82: groups are the
+ * positions along `dim` sharing an index value; every group is reduced with
+ * torch.softmax / torch.log_softmax / torch.logsumexp in float64.
+ * torch.softmax(v) = exp(v - max) / sum(exp(v - max)) with max the plain
+ * maximum (NaN if a NaN is present), so +-inf and NaN follow IEEE from there.
+ * mode 0 softmax, 1 log_softmax -> out [before, len, after];
+ * mode 2 logsumexp -> out [before, groups, after] (empty group -> -inf).
+ */
+void oracle_group_softmax(const float* src, const int64_t* index, int64_t before, int64_t len,
+                          int64_t after, int64_t groups, int mode, double* out) {
+  int64_t* cnt = (int64_t*)calloc((size_t)(groups + 1), sizeof(int64_t));
+  for (int64_t l = 0; l < len; ++l)
+    if (index[l] >= 0 && index[l] < groups) cnt[index[l] + 1]++;
+  for (int64_t g = 0; g < groups; ++g) cnt[g + 1] += cnt[g];
+  int64_t* pos = (int64_t*)malloc((size_t)(len > 0 ? len : 1) * sizeof(int64_t));
+  int64_t* fill = (int64_t*)calloc((size_t)(groups > 0 ? groups : 1), sizeof(int64_t));
+  for (int64_t l = 0; l < len; ++l) {
+    const int64_t g = index[l];
+    if (g >= 0 && g < groups) pos[cnt[g] + fill[g]++] = l;
+  }
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int64_t g = 0; g < groups; ++g) {
+    const int64_t* ps = pos + cnt[g];
+    const int64_t n = cnt[g + 1] - cnt[g];
+    for (int64_t b = 0; b < before; ++b)
+      for (int64_t f = 0; f < after; ++f) {
+        double m = -INFINITY;
+        int nan = 0;
+        for (int64_t i = 0; i < n; ++i) {
+          const double v = (double)src[(b * len + ps[i]) * after + f];
+          if (isnan(v)) nan = 1;
+          else if (v > m) m = v;
+        }
+        if (nan) m = NAN;
+        if (mode == 2) {
+          double r;
+          if (n == 0) r = -INFINITY;
+          else if (isnan(m)) r = NAN;
+          else if (isinf(m)) r = m;
+          else {
+            double s = 0.0;
+            for (int64_t i = 0; i < n; ++i) s += exp((double)src[(b * len + ps[i]) * after + f] - m);
+            r = m + log(s);
+          }
+          out[(b * groups + g) * after + f] = r;
+          continue;
+        }
+        double s = 0.0;
+        for (int64_t i = 0; i < n; ++i) s += exp((double)src[(b * len + ps[i]) * after + f] - m);
+        for (int64_t i = 0; i < n; ++i) {
+          const double v = (double)src[(b * len + ps[i]) * after + f] - m;
+          out[(b * len + ps[i]) * after + f] = mode == 0 ? exp(v) / s : v - log(s);
+        }
+      }
+  }
+  if (mode != 2) {
+    /* positions whose index is out of range keep 0 (golden result starts as zeros) */
+    for (int64_t l = 0; l < len; ++l)
+      if (index[l] < 0 || index[l] >= groups)
+        for (int64_t b = 0; b < before; ++b)
+          for (int64_t f = 0; f < after; ++f) out[(b * len + l) * after + f] = 0.0;
+  }
+  free(cnt);
+  free(pos);
+  free(fill);
 }

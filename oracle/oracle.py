@@ -48,6 +48,12 @@ def lib():
         l.oracle_ptr2ind.argtypes = [_i64p, i64, i64, _i64p]
         l.oracle_segment_csr.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, ctypes.c_int,
                                          _f64p, vp]
+        l.oracle_segment_coo.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, ctypes.c_int,
+                                         ctypes.c_int, _f64p, vp]
+        l.oracle_scatter.argtypes = [_f32p, _i64p, i64, i64, i64, i64, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_double, _f64p, vp]
+        l.oracle_segment_lse.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, _f64p]
+        l.oracle_group_softmax.argtypes = [_f32p, _i64p, i64, i64, i64, i64, ctypes.c_int, _f64p]
         _lib = l
     return _lib
 
@@ -139,6 +145,85 @@ def segment_csr(src, indptr, reduce="sum"):
     lib().oracle_segment_csr(np.ascontiguousarray(src.reshape(-1)), ip.reshape(-1), stride, batch,
                              length, feat, segs, r, out, _ptr(arg))
     return out, arg
+
+
+def _split(shape, dim):
+    before = int(np.prod(shape[:dim])) if dim > 0 else 1
+    after = int(np.prod(shape[dim + 1:])) if dim + 1 < len(shape) else 1
+    return before, shape[dim], after
+
+
+FINFO_MAX = {"float32": 3.4028234663852886e38, "float16": 65504.0, "bfloat16": 3.3895313892515355e38}
+
+
+def segment_coo(src, index, segments, reduce="sum", out=None):
+    """Ascend 950 segment_coo rules (reference csrc/npu/segment_coo/op_kernel/arch35/segment_coo.cpp:114-153).
+
+    index: [..., L] sorted along its last dim (reduction dim = index.ndim - 1),
+    leading dims 1 or equal to src's.  out: optional seed values (float64
+    array of the output shape).  Returns (values float64, arg int64 | None).
+    """
+    src = _np(src, np.float32)
+    idx = _np(index, np.int64)
+    dim = idx.ndim - 1
+    before, length, after = _split(src.shape, dim)
+    ib = int(np.prod(idx.shape[:-1])) if idx.ndim > 1 else 1
+    if ib not in (1, before):
+        raise ValueError("index leading dims must broadcast")
+    r = REDUCE[reduce]
+    shape = src.shape[:dim] + (segments,) + src.shape[dim + 1:]
+    o = np.zeros(shape, np.float64) if out is None else np.array(out, dtype=np.float64).reshape(shape).copy()
+    arg = np.zeros(shape, np.int64) if r >= 2 else None
+    lib().oracle_segment_coo(np.ascontiguousarray(src.reshape(-1)), np.ascontiguousarray(idx.reshape(-1)), ib,
+                             before, length, after, segments, r, 0 if out is None else 1, o, _ptr(arg))
+    return o, arg
+
+
+def scatter(src, index, dim, size, reduce="sum", out=None, dtype_name="float32"):
+    """torch_scatter fold (reference test/scatter/arch35/golden.py:35-127).
+
+    index must already have src's shape (broadcast by the caller).  reduce
+    codes as torch_scatter: sum/add/mean/min/max/mul.  Returns (values, arg|None).
+    """
+    src = _np(src, np.float32)
+    idx = np.ascontiguousarray(np.broadcast_to(_np(index, np.int64), src.shape))
+    before, length, after = _split(src.shape, dim)
+    code = {"sum": 0, "add": 0, "mean": 1, "min": 2, "max": 3, "mul": 4}[reduce]
+    shape = src.shape[:dim] + (size,) + src.shape[dim + 1:]
+    o = np.zeros(shape, np.float64) if out is None else np.array(out, dtype=np.float64).reshape(shape).copy()
+    arg = np.zeros(shape, np.int64) if code in (2, 3) else None
+    lib().oracle_scatter(np.ascontiguousarray(src.reshape(-1)), idx.reshape(-1), before, length, after, size,
+                         code, 0 if out is None else 1, FINFO_MAX[dtype_name], o, _ptr(arg))
+    return o, arg
+
+
+def segment_logsumexp(src, indptr):
+    """reference test/segment_logsumexp/golden.py:25-44 (1-D indptr along dim 0)."""
+    src = _np(src, np.float32)
+    ip = _np(indptr, np.int64).reshape(-1)
+    length = src.shape[0]
+    feat = int(np.prod(src.shape[1:])) if src.ndim > 1 else 1
+    segs = ip.shape[0] - 1
+    out = np.zeros((segs,) + src.shape[1:], np.float64)
+    lib().oracle_segment_lse(np.ascontiguousarray(src.reshape(-1)), ip, 0, 1, length, feat, segs, out)
+    return out
+
+
+def group_softmax(src, index, dim, groups, mode):
+    """Grouped softmax family (reference test/common/grouped_softmax_golden.py:31-82).
+
+    mode: "softmax", "log_softmax" (src-shaped output) or "logsumexp"
+    (output with src.size(dim) replaced by `groups`).
+    """
+    src = _np(src, np.float32)
+    idx = _np(index, np.int64).reshape(-1)
+    dim = dim % src.ndim
+    before, length, after = _split(src.shape, dim)
+    m = {"softmax": 0, "log_softmax": 1, "logsumexp": 2}[mode]
+    shape = src.shape if m < 2 else src.shape[:dim] + (groups,) + src.shape[dim + 1:]
+    out = np.zeros(shape, np.float64)
+    lib().oracle_group_softmax(np.ascontiguousarray(src.reshape(-1)), idx, before, length, after, groups, m, out)
+    return out
 
 
 def threads() -> int:

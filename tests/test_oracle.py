@@ -239,3 +239,162 @@ def test_segment_broadcast_batched_pointer():
     s64 = src.astype(np.float64)
     ref = np.stack([s64[:, 0:3].sum(1), np.zeros((3, 4)), s64[:, 3:10].sum(1)], axis=1)
     np.testing.assert_allclose(out, ref, rtol=1e-6)
+
+
+# ----------------------------------------------------------------- segment_coo (Ascend 950 rules)
+@pytest.mark.parametrize("mode", ["sum", "mean", "min", "max"])
+def test_segment_coo_unequal_segments_kat(mode):
+    # reference test/segment_coo/arch35/test_segment_coo.py:892-911
+    x = np.array([[2, 5], [2, 1], [3, 6], [4, 6], [1, 2]], dtype=np.float32)
+    idx = np.array([0, 0, 2, 2, 2])
+    out, arg = orc.segment_coo(x, idx, 4, mode)
+    ref = {"sum": [[4, 6], [0, 0], [8, 14], [0, 0]], "mean": [[2, 3], [0, 0], [8 / 3, 14 / 3], [0, 0]],
+           "min": [[2, 1], [0, 0], [1, 2], [0, 0]], "max": [[2, 5], [0, 0], [4, 6], [0, 0]]}[mode]
+    np.testing.assert_allclose(out, ref, rtol=1e-12)
+    if arg is not None:
+        expected = {"min": [[1, 1], [5, 5], [4, 4], [5, 5]], "max": [[1, 0], [5, 5], [3, 3], [5, 5]]}[mode]
+        np.testing.assert_array_equal(arg, expected)
+
+
+def test_segment_coo_matches_segment_reduce_and_later_tie_rule():
+    rng = np.random.default_rng(11)
+    idx = np.sort(rng.integers(0, 30, 400))
+    src = rng.integers(-3, 4, size=(2, 400, 3)).astype(np.float32)  # ties everywhere
+    lengths = np.bincount(idx, minlength=30)
+    for mode in ("sum", "mean", "min", "max"):
+        out, arg = orc.segment_coo(src, idx[None, :], 30, mode)
+        ref = torch.segment_reduce(torch.from_numpy(src).double(), mode,
+                                   lengths=torch.from_numpy(np.tile(lengths, (2, 1))), axis=1, unsafe=True).numpy()
+        ref[:, lengths == 0] = 0.0
+        np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+        if arg is not None:
+            ptr = np.concatenate([[0], np.cumsum(lengths)])
+            for b in range(2):
+                for s in range(30):
+                    for f in range(3):
+                        a, z = ptr[s], ptr[s + 1]
+                        if a == z:
+                            assert arg[b, s, f] == 400
+                        else:
+                            hits = np.nonzero(src[b, a:z, f] == out[b, s, f])[0]
+                            assert arg[b, s, f] == a + hits[-1]  # the LAST extremum
+
+
+def test_segment_coo_out_seeds():
+    x = np.array([[1.0], [5.0], [2.0]], dtype=np.float32)
+    idx = np.array([0, 0, 2])
+    seed = np.array([[3.0], [7.0], [-1.0]])
+    out, arg = orc.segment_coo(x, idx, 3, "max", out=seed)
+    np.testing.assert_array_equal(out, [[5.0], [7.0], [2.0]])
+    np.testing.assert_array_equal(arg, [[1], [3], [2]])
+    out, _ = orc.segment_coo(x, idx, 3, "mean", out=seed)
+    np.testing.assert_allclose(out, [[(3 + 1 + 5) / 2], [7.0], [(-1 + 2) / 1]])
+    out, _ = orc.segment_coo(x, idx, 3, "sum", out=seed)  # sum overwrites
+    np.testing.assert_array_equal(out, [[6.0], [0.0], [2.0]])
+
+
+# ----------------------------------------------------------------- scatter (torch_scatter)
+def test_scatter_later_writer_tie_kat():
+    # reference test/scatter/arch35/test_scatter.py:322-331
+    src = np.array([4.0, 2.0, 2.0, 5.0, 5.0], dtype=np.float32)
+    index = np.array([0, 0, 0, 1, 1])
+    mn, amin = orc.scatter(src, index, 0, 2, "min")
+    mx, amax = orc.scatter(src, index, 0, 2, "max")
+    np.testing.assert_array_equal(mn, [2.0, 5.0])
+    np.testing.assert_array_equal(mx, [4.0, 5.0])
+    np.testing.assert_array_equal(amin, [2, 4])
+    np.testing.assert_array_equal(amax, [0, 4])
+
+
+def test_scatter_docs_example():
+    # reference docs/en/api_reference.md:1032-1048
+    src = np.array([1.0, 2.0, 3.0, 4.0], dtype=np.float32)
+    index = np.array([0, 1, 0, 1])
+    np.testing.assert_array_equal(orc.scatter(src, index, 0, 2, "sum")[0], [4.0, 6.0])
+    v, a = orc.scatter(src, index, 0, 2, "max")
+    np.testing.assert_array_equal(v, [3.0, 4.0])
+    np.testing.assert_array_equal(a, [2, 3])
+
+
+@pytest.mark.parametrize("reduce,torch_reduce", [("sum", "sum"), ("mean", "mean"), ("min", "amin"),
+                                                 ("max", "amax"), ("mul", "prod")])
+def test_scatter_matches_torch_scatter_reduce(reduce, torch_reduce):
+    rng = np.random.default_rng(12)
+    src = rng.standard_normal((3, 50, 4)).astype(np.float32)
+    index = rng.integers(0, 12, size=(3, 50, 4))
+    out, arg = orc.scatter(src, index, 1, 15, reduce)
+    ref = torch.zeros(3, 15, 4, dtype=torch.float64).scatter_reduce(
+        1, torch.from_numpy(index), torch.from_numpy(src).double(), torch_reduce, include_self=False)
+    written = torch.zeros(3, 15, 4, dtype=torch.bool).scatter_(1, torch.from_numpy(index), True).numpy()
+    ref = ref.numpy()
+    if reduce == "mul":
+        ref = np.where(written, ref, 1.0)
+    else:
+        ref = np.where(written, ref, 0.0)
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+    if arg is not None:
+        for b in range(3):
+            for t in range(15):
+                for f in range(4):
+                    hits = [l for l in range(50) if index[b, l, f] == t and src[b, l, f] == out[b, t, f]]
+                    assert arg[b, t, f] == (hits[-1] if hits else 50)
+
+
+def test_scatter_out_is_accumulated():
+    src = np.array([1.0, 2.0, 3.0], dtype=np.float32)
+    index = np.array([0, 0, 1])
+    seed = np.array([10.0, 20.0, 30.0])
+    np.testing.assert_array_equal(orc.scatter(src, index, 0, 3, "sum", out=seed)[0], [13.0, 23.0, 30.0])
+    np.testing.assert_allclose(orc.scatter(src, index, 0, 3, "mean", out=seed)[0], [13 / 2, 23.0, 30.0])
+    v, a = orc.scatter(src, index, 0, 3, "max", out=seed)
+    np.testing.assert_array_equal(v, [10.0, 20.0, 30.0])
+    np.testing.assert_array_equal(a, [3, 3, 3])
+
+
+# ----------------------------------------------------------------- log-sum-exp / grouped softmax
+def test_segment_logsumexp_matches_torch():
+    rng = np.random.default_rng(13)
+    lengths = rng.poisson(4, size=40)
+    lengths[::9] = 0
+    src = (rng.standard_normal((int(lengths.sum()), 5)) * 30).astype(np.float32)
+    ptr = np.concatenate([[0], np.cumsum(lengths)])
+    out = orc.segment_logsumexp(src, ptr)
+    for s in range(40):
+        a, z = ptr[s], ptr[s + 1]
+        ref = torch.logsumexp(torch.from_numpy(src[a:z]).double(), 0).numpy() if z > a else np.full(5, -np.inf)
+        np.testing.assert_allclose(out[s], ref, rtol=1e-12)
+
+
+def test_segment_logsumexp_special_values():
+    src = np.array([[-np.inf], [-np.inf], [np.inf], [1.0], [np.nan], [2.0]], dtype=np.float32)
+    out = orc.segment_logsumexp(src, np.array([0, 2, 4, 6, 6]))
+    assert out[0, 0] == -np.inf and out[1, 0] == np.inf and np.isnan(out[2, 0]) and out[3, 0] == -np.inf
+
+
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+def test_group_softmax_matches_torch_per_group(mode):
+    rng = np.random.default_rng(14)
+    src = (rng.standard_normal((2, 30, 3)) * 5).astype(np.float32)
+    index = rng.integers(0, 8, size=30)
+    index[index == 5] = 6  # group 5 empty
+    out = orc.group_softmax(src, index, 1, 8, mode)
+    t = torch.from_numpy(src).double()
+    for g in range(8):
+        pos = np.nonzero(index == g)[0]
+        if mode == "logsumexp":
+            ref = torch.logsumexp(t[:, pos], 1).numpy() if pos.size else np.full((2, 3), -np.inf)
+            np.testing.assert_allclose(out[:, g], ref, rtol=1e-12)
+        elif pos.size:
+            fn = torch.softmax if mode == "softmax" else torch.log_softmax
+            np.testing.assert_allclose(out[:, pos], fn(t[:, pos], 1).numpy(), rtol=1e-12, atol=1e-15)
+
+
+def test_group_softmax_special_values_follow_torch():
+    src = np.array([np.inf, 1.0, -np.inf, 2.0, np.nan, 0.0, -np.inf, -np.inf], dtype=np.float32)
+    index = np.array([0, 0, 1, 1, 2, 2, 3, 3])
+    t = torch.from_numpy(src).double()
+    for mode, fn in (("softmax", torch.softmax), ("log_softmax", torch.log_softmax)):
+        out = orc.group_softmax(src, index, 0, 4, mode)
+        ref = np.concatenate([fn(t[2 * g:2 * g + 2], 0).numpy() for g in range(4)])
+        np.testing.assert_array_equal(np.isnan(out), np.isnan(ref))
+        np.testing.assert_allclose(out[~np.isnan(ref)], ref[~np.isnan(ref)])

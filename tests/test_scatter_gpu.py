@@ -1,0 +1,182 @@
+"""GPU parity of the scatter family and the grouped softmax family against the
+oracle.  Both execution paths are covered: a sorted 1-D index (segment
+engine) and unsorted / full-shape indices (atomic kernels).  Cases follow the
+reference tests (test/scatter/arch35/test_scatter.py,
+test/scatter_softmax/*, test/scatter_log_softmax/*, test/scatter_logsumexp/*).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_exact, assert_sum_close, cast_like
+
+pytestmark = pytest.mark.gpu
+
+DT = [torch.float32, torch.float16, torch.bfloat16]
+SOFT_TOL = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+INF, NAN = float("inf"), float("nan")
+
+
+def test_later_writer_tie_kat(ogn):
+    # reference test/scatter/arch35/test_scatter.py:322-331
+    src = torch.tensor([4.0, 2.0, 2.0, 5.0, 5.0], device="cuda")
+    index = torch.tensor([0, 0, 0, 1, 1], device="cuda")
+    min_out, arg_min = ogn.scatter_min(src, index)
+    max_out, arg_max = ogn.scatter_max(src, index)
+    assert torch.equal(min_out.cpu(), torch.tensor([2.0, 5.0]))
+    assert torch.equal(max_out.cpu(), torch.tensor([4.0, 5.0]))
+    assert torch.equal(arg_min.cpu(), torch.tensor([2, 4]))
+    assert torch.equal(arg_max.cpu(), torch.tensor([0, 4]))
+    # same data, unsorted order -> atomic path
+    perm = torch.tensor([3, 0, 4, 1, 2], device="cuda")
+    v, a = ogn.scatter_min(src[perm], index[perm])
+    assert torch.equal(v.cpu(), torch.tensor([2.0, 5.0])) and torch.equal(a.cpu(), torch.tensor([4, 2]))
+
+
+def test_docs_example(ogn):
+    # reference docs/en/api_reference.md:1032-1048
+    src = torch.tensor([1.0, 2.0, 3.0, 4.0], device="cuda")
+    index = torch.tensor([0, 1, 0, 1], device="cuda")
+    assert torch.equal(ogn.scatter_sum(src, index).cpu(), torch.tensor([4.0, 6.0]))
+    values, arg = ogn.scatter_max(src, index)
+    assert torch.equal(values.cpu(), torch.tensor([3.0, 4.0])) and torch.equal(arg.cpu(), torch.tensor([2, 3]))
+
+
+def _check(ogn, oracle, src, index, dim, size, reduce, out=None, what=""):
+    fn = {"sum": ogn.scatter_sum, "mean": ogn.scatter_mean, "mul": ogn.scatter_mul,
+          "min": ogn.scatter_min, "max": ogn.scatter_max}[reduce]
+    dev_out = None if out is None else out.clone().cuda()
+    res = fn(src.cuda(), index.cuda(), dim, dev_out, size)
+    got, arg = res if isinstance(res, tuple) else (res, None)
+    if dev_out is not None:
+        assert got.data_ptr() == dev_out.data_ptr()
+    d = dim % src.dim()
+    from ops_gnn.scatter import broadcast
+    idx_b = broadcast(index, src, d)
+    name = {torch.float32: "float32", torch.float16: "float16", torch.bfloat16: "bfloat16"}[src.dtype]
+    gold, garg = oracle.scatter(src, idx_b, d, size, reduce, None if out is None else out.double().numpy(), name)
+    if reduce in ("min", "max"):
+        assert_exact(got, cast_like(gold, src.dtype), what + " values")
+        assert_exact(arg, garg, what + " arg")
+    elif reduce == "mul":
+        np.testing.assert_allclose(got.float().cpu().numpy(), cast_like(gold, src.dtype), rtol=2e-2 if src.dtype != torch.float32 else 1e-3, atol=1e-6)
+    else:
+        sc, _ = oracle.scatter(src.float().abs(), idx_b, d, size, reduce,
+                               None if out is None else out.double().abs().numpy(), name)
+        assert_sum_close(got, gold, sc, src.dtype, what)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max", "mul"])
+@pytest.mark.parametrize("sorted_index", [True, False])
+def test_compact_index(ogn, oracle, dtype, reduce, sorted_index):
+    rng = np.random.default_rng(41)
+    idx = rng.integers(0, 300, 5000)
+    idx[:1500] = 7  # hot target
+    if sorted_index:
+        idx = np.sort(idx)
+    src_np = rng.integers(-3, 4, size=(5000, 16)).astype(np.float32)
+    if reduce == "mul":
+        src_np = rng.uniform(0.9, 1.1, size=(5000, 16)).astype(np.float32)
+    src = torch.from_numpy(src_np).to(dtype)
+    _check(ogn, oracle, src, torch.from_numpy(idx), 0, 310, reduce, what=f"{reduce}/{sorted_index}")
+
+
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("sorted_index", [True, False])
+def test_out_is_accumulated(ogn, oracle, reduce, sorted_index):
+    rng = np.random.default_rng(42)
+    idx = rng.integers(0, 50, 800)
+    if sorted_index:
+        idx = np.sort(idx)
+    src = torch.from_numpy(rng.standard_normal((800, 8)).astype(np.float32))
+    out = torch.from_numpy(rng.standard_normal((60, 8)).astype(np.float32))
+    _check(ogn, oracle, src, torch.from_numpy(idx), 0, 60, reduce, out=out, what=f"out/{reduce}")
+
+
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+def test_full_shape_index_and_negative_dim(ogn, oracle, reduce):
+    rng = np.random.default_rng(43)
+    src = torch.from_numpy(rng.standard_normal((3, 40, 6)).astype(np.float32))
+    index = torch.from_numpy(rng.integers(0, 9, size=(3, 40, 6)))
+    _check(ogn, oracle, src, index, -2, 9, reduce, what="full")
+    # 1-D index along the last dim
+    idx1 = torch.from_numpy(rng.integers(0, 4, size=6))
+    _check(ogn, oracle, src, idx1, -1, 4, reduce, what="last dim")
+
+
+def test_scatter_dim_size_inference_and_empty(ogn):
+    src = torch.randn(5, 3, device="cuda")
+    out = ogn.scatter(src, torch.tensor([0, 4, 4, 1, 0], device="cuda"), dim=0)
+    assert out.shape == (5, 3)
+    empty = ogn.scatter(torch.empty(0, 3, device="cuda"), torch.empty(0, dtype=torch.long, device="cuda"), 0,
+                        dim_size=4)
+    assert empty.shape == (4, 3) and bool((empty == 0).all())
+    with pytest.raises(ValueError):
+        ogn.scatter(src, torch.zeros(5, dtype=torch.long, device="cuda"), reduce="median")
+    with pytest.raises(TypeError):
+        ogn.scatter(src, torch.zeros(5, dtype=torch.int32, device="cuda"))
+
+
+# ----------------------------------------------------------------- grouped softmax family
+def _softmax_check(ogn, oracle, src, index, dim, groups, mode, tol):
+    fn = {"softmax": ogn.scatter_softmax, "log_softmax": ogn.scatter_log_softmax,
+          "logsumexp": ogn.scatter_logsumexp}[mode]
+    got = fn(src.cuda(), index.cuda(), dim, groups)
+    gold = cast_like(oracle.group_softmax(src, index.long(), dim, groups, mode), src.dtype)
+    g = got.float().cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(g), np.isnan(gold))
+    np.testing.assert_allclose(g, gold, rtol=tol, atol=tol, equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+@pytest.mark.parametrize("sorted_index", [True, False])
+@pytest.mark.parametrize("index_dtype", [torch.int64, torch.int32])
+def test_grouped_softmax(ogn, oracle, dtype, mode, sorted_index, index_dtype):
+    rng = np.random.default_rng(51)
+    idx = rng.integers(0, 64, 3000)
+    idx[idx == 9] = 10  # an empty group
+    if sorted_index:
+        idx = np.sort(idx)
+    src = torch.from_numpy((rng.standard_normal((2, 3000, 5)) * 6).astype(np.float32)).to(dtype)
+    _softmax_check(ogn, oracle, src, torch.from_numpy(idx).to(index_dtype), 1, 64, mode, SOFT_TOL[dtype])
+
+
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+def test_grouped_softmax_edge_rows(ogn, oracle, mode):
+    # GAT layout: one score per edge, grouped by destination row
+    rng = np.random.default_rng(52)
+    deg = rng.poisson(40, size=500)
+    deg[::50] = 4000
+    idx = np.repeat(np.arange(500), deg)
+    src = torch.from_numpy((rng.standard_normal(idx.size) * 3).astype(np.float32))
+    _softmax_check(ogn, oracle, src, torch.from_numpy(idx), 0, 500, mode, 1e-5)
+
+
+@pytest.mark.parametrize("sorted_index", [True, False])
+def test_grouped_softmax_special_values(ogn, oracle, sorted_index):
+    src = torch.tensor([INF, 1.0, -INF, 2.0, NAN, 0.0, -INF, -INF])
+    index = torch.tensor([0, 0, 1, 1, 2, 2, 3, 3])
+    if not sorted_index:
+        perm = torch.tensor([5, 2, 7, 0, 3, 6, 1, 4])
+        src, index = src[perm], index[perm]
+    for mode in ("softmax", "log_softmax", "logsumexp"):
+        _softmax_check(ogn, oracle, src, index, 0, 4, mode, 1e-6)
+
+
+def test_grouped_softmax_errors(ogn):
+    src = torch.randn(6, device="cuda")
+    with pytest.raises(ValueError, match="non-negative"):
+        ogn.scatter_softmax(src, torch.tensor([0, -1, 0, 0, 0, 0], device="cuda"))
+    with pytest.raises(ValueError, match="smaller than dim_size"):
+        ogn.scatter_softmax(src, torch.tensor([0, 3, 0, 0, 0, 0], device="cuda"), dim_size=2)
+    with pytest.raises(ValueError, match="must match"):
+        ogn.scatter_log_softmax(src, torch.tensor([0, 1], device="cuda"))
+    with pytest.raises(ValueError, match="1-D"):
+        ogn.scatter_logsumexp(src, torch.zeros(2, 3, dtype=torch.long, device="cuda"))
+    with pytest.raises(TypeError):
+        ogn.scatter_softmax(src.double(), torch.zeros(6, dtype=torch.long, device="cuda"))
+    with pytest.raises(IndexError):
+        ogn.scatter_softmax(src, torch.zeros(6, dtype=torch.long, device="cuda"), dim=3)
