@@ -128,8 +128,11 @@ def test_segment_csr_empty_and_errors(ogn):
         ogn.segment_csr(torch.ones(4, 2, device="cuda"), torch.tensor([0, 4], dtype=torch.int32, device="cuda"))
     with pytest.raises(RuntimeError, match="nondecreasing"):
         ogn.segment_csr(torch.ones(4, 2, device="cuda"), torch.tensor([0, 3, 2], device="cuda"))
-    with pytest.raises(RuntimeError, match="nondecreasing"):
-        ogn.segment_csr(torch.ones(4, 2, device="cuda"), torch.tensor([0, 5], device="cuda"))
+    with pytest.raises(RuntimeError, match="non-negative"):
+        ogn.segment_csr(torch.ones(4, 2, device="cuda"), torch.tensor([-1, 3], device="cuda"))
+    # ends past src.size(dim) are clamped
+    out = ogn.segment_csr(torch.ones(4, 2, device="cuda"), torch.tensor([0, 3, 9], device="cuda"))
+    assert out.cpu().tolist() == [[3.0, 3.0], [1.0, 1.0]]
     with pytest.raises(ValueError, match="not valid"):
         ogn.segment_csr(torch.ones(4, 2, device="cuda"), torch.tensor([0, 4], device="cuda"), reduce="mul")
     with pytest.raises(TypeError):
