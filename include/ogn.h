@@ -117,6 +117,43 @@ int ogn_spmm_csr(const void* rowptr, const void* col, int index_dtype, const voi
                  int64_t* arg, int reduce, void* workspace, size_t workspace_bytes,
                  void* stream);
 
+/* Generalised CSR aggregation (DGL-style spmm / bspmm):
+ *   out[b, r, k] = R_{e in row r} msg(mat[b, col[e], k], value[e, (k | 0)])
+ * msg: OGN_MSG_MUL (x * w; w = 1 without value), OGN_MSG_ADD (x + w),
+ * OGN_MSG_SUB (x - w), OGN_MSG_DIV (x / w).
+ * semantics: OGN_SPMM_TORCH_SPARSE (as ogn_spmm_csr) or OGN_SPMM_DGL
+ * (reference python/ops_gnn/spmm.py:148-208, csrc/npu/common/spmm/spmm_utils.h:389-406:
+ * min/max propagate NaN -- a row holding a NaN message gives NaN -- empty rows
+ * give 0, and arg may be NULL).  Replaces RunSpmmCopyLhs / UnifiedSpmmCsr
+ * (reference csrc/npu/common/spmm/spmm_utils.h:188-204,
+ * csrc/npu/unified_spmm/op_host/unified_spmm.cpp:116-158) and the torch
+ * composition for binary messages (python/ops_gnn/spmm.py:148-208); fp16
+ * accumulates in fp32.  Workspace: ogn_spmm_csr_workspace_size(). */
+enum { OGN_MSG_MUL = 0, OGN_MSG_ADD = 1, OGN_MSG_SUB = 2, OGN_MSG_DIV = 3 };
+enum { OGN_SPMM_TORCH_SPARSE = 0, OGN_SPMM_DGL = 1 };
+int ogn_spmm_csr_ex(const void* rowptr, const void* col, int index_dtype, const void* value,
+                    int64_t value_width, const void* mat, int in_dtype, int64_t batch, int64_t m,
+                    int64_t n, int64_t k, int64_t nnz, void* out, int out_dtype, int64_t* arg,
+                    int reduce, int message_op, int semantics, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* ------------------------------------------------------------------ SDDMM
+ * out[e] = phi(lhs[t_l(e)], rhs[t_r(e)]) on a CSR graph (reference
+ * SddmmCsrForward csrc/npu/sddmm_csr/op_host/sddmm_csr.cpp:415-461, golden
+ * test/sddmm_csr/arch22/golden.py:74-90).  Targets: 0 = row of e (src),
+ * 1 = e (edge), 2 = col[e] (dst).  lhs [lhs_rows, k], rhs [rhs_rows, k],
+ * both of `dtype` (f32/f16/bf16).  op: OGN_SDDMM_DOT -> out [nnz] (feature
+ * reduction), ADD/SUB/MUL/DIV -> out [nnz, k], COPY_LHS / COPY_RHS -> the
+ * gathered operand [nnz, k] (the unused operand may be NULL).  fp32 compute,
+ * one rounding to dtype.  Workspace: ogn_sddmm_csr_workspace_size(). */
+enum { OGN_SDDMM_DOT = 0, OGN_SDDMM_ADD = 1, OGN_SDDMM_SUB = 2, OGN_SDDMM_MUL = 3, OGN_SDDMM_DIV = 4,
+       OGN_SDDMM_COPY_LHS = 5, OGN_SDDMM_COPY_RHS = 6 };
+size_t ogn_sddmm_csr_workspace_size(int64_t nnz, int64_t k, int dtype);
+int ogn_sddmm_csr(const void* rowptr, const void* col, int index_dtype, int64_t m, int64_t nnz,
+                  const void* lhs, int64_t lhs_rows, int lhs_target, const void* rhs, int64_t rhs_rows,
+                  int rhs_target, int64_t k, int dtype, int op, void* out, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ index conversion
  * ind2ptr: out[i] = #{ j : ind[j] < i } for i in [0, rows]; `ind` sorted
  * non-decreasing (numel entries).  out: int64 [rows + 1].  numel == 0 gives
@@ -161,6 +198,8 @@ int ogn_ptr2ind(const void* ptr, int index_dtype, int64_t rows, int64_t numel, i
  *    (empty: out unchanged); min/max fold with <= / >= from out (or from the
  *    dtype's finite extreme, a position never written giving 0), last
  *    extremum wins, arg = length when nothing was taken.
+ *  OGN_SEM_DGL -- DGL copy_rhs aggregation (reference python/ops_gnn/spmm.py:165-208):
+ *    min/max propagate NaN, empty segments give 0.
  *  reduce = lse gives log(sum(exp(x))) with the shift clamped to +-FLT_MAX
  *    (reference csrc/npu/segment_logsumexp/op_kernel/common/segment_logsumexp_kernel.h:10-45);
  *    empty segments give -inf.
@@ -168,7 +207,7 @@ int ogn_ptr2ind(const void* ptr, int index_dtype, int64_t rows, int64_t numel, i
  * pairs (reference csrc/npu/segment_csr/op_host/segment_csr.cpp:1663-1702,
  * csrc/npu/segment_coo/op_host/segment_coo.cpp:1127-1175).
  */
-enum { OGN_SEM_SEGMENT_CSR = 0, OGN_SEM_SEGMENT_COO = 1, OGN_SEM_SCATTER = 2 };
+enum { OGN_SEM_SEGMENT_CSR = 0, OGN_SEM_SEGMENT_COO = 1, OGN_SEM_SCATTER = 2, OGN_SEM_DGL = 3 };
 enum { OGN_SEG_HAS_OUT = 1 };
 size_t ogn_segment_reduce_workspace_size(int64_t batch, int64_t length, int64_t segments, int64_t k,
                                          int64_t ptr_batches, int dtype, int reduce);

@@ -48,8 +48,21 @@ enum { RK_SUM = 0, RK_MINMAX = 1, RK_LSE = 2 };
 enum {
   MM_SPMM = 0,    // torch_sparse: NaN ignored, first tie, none -> 0 / arg_empty
   MM_SEGCSR = 1,  // segment_csr: strict improvement from +-inf (arg = segment start)
-  MM_LATER = 2    // segment_coo / scatter: fold from a seed with >= / <=, later tie
+  MM_LATER = 2,   // segment_coo / scatter: fold from a seed with >= / <=, later tie
+  MM_NANPROP = 3  // DGL spmm: a NaN message makes the result NaN; empty -> 0, no arg
 };
+// Message = x (op) w for each position (w = edge weight, 1 when absent).
+enum { OP_MUL = 0, OP_ADD = 1, OP_SUB = 2, OP_DIV = 3 };
+
+template <typename T>
+__device__ __forceinline__ T apply_op(T x, T w, int op) {
+  switch (op) {
+    case OP_ADD: return x + w;
+    case OP_SUB: return x - w;
+    case OP_DIV: return x / w;
+    default: return x * w;
+  }
+}
 // Seeds for MM_LATER.
 enum {
   SEED_NONE = 0,
@@ -64,6 +77,7 @@ struct Params {
   const void* col;      // gather mode
   const void* val;
   int val_mode;         // 0 none, 1 one weight per position, 2 k weights per position
+  int val_op;           // OP_*: how a weight combines with the gathered feature
   const void* src;
   int src_dt;
   int64_t src_bstride;  // elements between batches of src
@@ -152,7 +166,7 @@ __device__ __forceinline__ void finish_elem(const Params& p, int64_t b, int64_t 
   } else {
     const bool is_min = p.reduce == OGN_REDUCE_MIN;
     const bool has = barg != kNone;
-    if (p.mm_mode == MM_SPMM) {
+    if (p.mm_mode == MM_SPMM || p.mm_mode == MM_NANPROP) {
       *outv = has ? (float)best : 0.f;
       *outarg = has ? barg : p.arg_empty;
     } else if (p.mm_mode == MM_SEGCSR) {
@@ -235,6 +249,8 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
   const bool is_min = p.reduce == OGN_REDUCE_MIN;
   const bool is_prod = p.reduce == OGN_REDUCE_PROD;
   const bool later = p.mm_mode == MM_LATER;
+  const bool nanprop = p.mm_mode == MM_NANPROP;
+  const int vop = p.val_op;
 
   const int64_t base = ptr[0];
   const int64_t end = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[M] - base, p.nnz_bound), 0);
@@ -286,7 +302,9 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
                                              : shflf((float)best[i], lane ^ off));
           const int64_t oa = shfl64(barg[i], lane ^ off);
           bool take;
-          if (later) {
+          if (nanprop) {
+            take = oa != kNone && (barg[i] == kNone || (ob != ob) || better(ob, best[i], is_min));
+          } else if (later) {
             take = oa != kNone && (barg[i] == kNone || better(ob, best[i], is_min) ||
                                    (ob == best[i] && oa > barg[i]));
           } else {
@@ -420,8 +438,13 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
             for (int i = 0; i < NE; ++i) {
               const float wi = w[u][VL ? i : 0];
               if constexpr (RK == RK_MINMAX) {
-                const MT pv = (MT)x[u][i] * (MT)wi;
-                if (!(pv != pv)) {
+                const MT pv = apply_op<MT>((MT)x[u][i], (MT)wi, vop);
+                if (nanprop) {
+                  if (barg[i] == kNone || (pv != pv) || better(pv, best[i], is_min)) {
+                    best[i] = pv;
+                    barg[i] = e_mine;
+                  }
+                } else if (!(pv != pv)) {
                   const bool take = barg[i] == kNone || better(pv, best[i], is_min) ||
                                     (later && pv == best[i]);
                   if (take) {
@@ -431,10 +454,14 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
                 }
               } else if constexpr (RK == RK_LSE) {
                 float m = (float)best[i];
-                lse_add(m, acc[i], x[u][i] * wi);
+                lse_add(m, acc[i], apply_op<float>(x[u][i], wi, vop));
                 best[i] = m;
               } else {
-                acc[i] = is_prod ? acc[i] * (x[u][i] * wi) : __builtin_fmaf(x[u][i], wi, acc[i]);
+                if (vop == OP_MUL)
+                  acc[i] = is_prod ? acc[i] * (x[u][i] * wi) : __builtin_fmaf(x[u][i], wi, acc[i]);
+                else
+                  acc[i] = is_prod ? acc[i] * apply_op<float>(x[u][i], wi, vop)
+                                   : acc[i] + apply_op<float>(x[u][i], wi, vop);
               }
             }
             added = true;
@@ -486,6 +513,7 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   const bool is_min = p.reduce == OGN_REDUCE_MIN;
   const bool is_prod = p.reduce == OGN_REDUCE_PROD;
   const bool later = p.mm_mode == MM_LATER;
+  const bool nanprop = p.mm_mode == MM_NANPROP;
   constexpr int kBatch = 8;
   for (int64_t k = lane; k < K; k += kWave) {
     const int64_t base_rec = (b * p.nchunks) * K + k;
@@ -530,7 +558,8 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
           const MT ob = (MT)vd[j];
           const int64_t oa = vg[j];
           // later records hold later positions
-          if (oa != kNone && (barg == kNone || better(ob, best, is_min) || (later && ob == best))) {
+          if (oa != kNone && !(nanprop && best != best) &&
+              (barg == kNone || better(ob, best, is_min) || (later && ob == best) || (nanprop && ob != ob))) {
             best = ob;
             barg = oa;
           }

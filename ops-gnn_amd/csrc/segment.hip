@@ -89,7 +89,7 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
     return fail(OGN_EUNSUPPORTED, "ogn_segment_reduce: src dtype must be float32, float16 or bfloat16");
   if (reduce < OGN_REDUCE_SUM || reduce > OGN_REDUCE_LSE)
     return fail(OGN_EINVAL, "ogn_segment_reduce: unknown reduce code");
-  if (semantics < OGN_SEM_SEGMENT_CSR || semantics > OGN_SEM_SCATTER)
+  if (semantics < OGN_SEM_SEGMENT_CSR || semantics > OGN_SEM_DGL)
     return fail(OGN_EINVAL, "ogn_segment_reduce: unknown semantics code");
   if (ptr_batches != 1 && ptr_batches != batch)
     return fail(OGN_EINVAL, "ogn_segment_reduce: ptr_batches must be 1 or batch");
@@ -121,6 +121,9 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
   switch (semantics) {
     case OGN_SEM_SEGMENT_CSR:
       p.mm_mode = MM_SEGCSR;
+      break;
+    case OGN_SEM_DGL:
+      p.mm_mode = MM_NANPROP;
       break;
     case OGN_SEM_SEGMENT_COO:
       p.mm_mode = MM_LATER;

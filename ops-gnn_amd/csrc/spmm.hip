@@ -22,10 +22,40 @@ size_t ogn_spmm_csr_workspace_size(int64_t m, int64_t nnz, int64_t k, int64_t ba
   return std::max(workspace_layout(pa, k, batch, 1, rk).total, workspace_layout(pu, k, batch, 1, rk).total);
 }
 
+static int spmm_impl(const void* rowptr, const void* col, int index_dtype, const void* value, int64_t value_width,
+                     const void* mat, int in_dtype, int64_t batch, int64_t m, int64_t n, int64_t k, int64_t nnz,
+                     void* out, int out_dtype, int64_t* arg, int reduce, int message_op, int semantics,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 int ogn_spmm_csr(const void* rowptr, const void* col, int index_dtype, const void* value,
                  int64_t value_width, const void* mat, int in_dtype, int64_t batch, int64_t m,
                  int64_t n, int64_t k, int64_t nnz, void* out, int out_dtype, int64_t* arg,
                  int reduce, void* workspace, size_t workspace_bytes, void* stream) {
+  return spmm_impl(rowptr, col, index_dtype, value, value_width, mat, in_dtype, batch, m, n, k, nnz, out,
+                   out_dtype, arg, reduce, OGN_MSG_MUL, OGN_SPMM_TORCH_SPARSE, workspace, workspace_bytes,
+                   stream);
+}
+
+int ogn_spmm_csr_ex(const void* rowptr, const void* col, int index_dtype, const void* value,
+                    int64_t value_width, const void* mat, int in_dtype, int64_t batch, int64_t m,
+                    int64_t n, int64_t k, int64_t nnz, void* out, int out_dtype, int64_t* arg,
+                    int reduce, int message_op, int semantics, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (message_op < OGN_MSG_MUL || message_op > OGN_MSG_DIV)
+    return fail(OGN_EINVAL, "ogn_spmm_csr_ex: unknown message op");
+  if (semantics != OGN_SPMM_TORCH_SPARSE && semantics != OGN_SPMM_DGL)
+    return fail(OGN_EINVAL, "ogn_spmm_csr_ex: unknown semantics");
+  return spmm_impl(rowptr, col, index_dtype, value, value_width, mat, in_dtype, batch, m, n, k, nnz, out,
+                   out_dtype, arg, reduce, message_op, semantics, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+static int spmm_impl(const void* rowptr, const void* col, int index_dtype, const void* value,
+                 int64_t value_width, const void* mat, int in_dtype, int64_t batch, int64_t m,
+                 int64_t n, int64_t k, int64_t nnz, void* out, int out_dtype, int64_t* arg,
+                 int reduce, int message_op, int semantics, void* workspace, size_t workspace_bytes,
+                 void* stream) {
   if (m < 0 || n < 0 || k < 0 || nnz < 0 || batch < 0)
     return fail(OGN_EINVAL, "ogn_spmm_csr: negative size");
   if (index_dtype != OGN_I32 && index_dtype != OGN_I64)
@@ -38,7 +68,8 @@ int ogn_spmm_csr(const void* rowptr, const void* col, int index_dtype, const voi
     return fail(OGN_EINVAL, "ogn_spmm_csr: reduce must be sum/mean/min/max");
   const bool mm = reduce >= OGN_REDUCE_MIN;
   if (m == 0 || k == 0 || batch == 0) return OGN_OK;
-  if (!rowptr || !out || (mm && !arg)) return fail(OGN_EINVAL, "ogn_spmm_csr: null pointer");
+  if (!rowptr || !out || (mm && !arg && semantics == OGN_SPMM_TORCH_SPARSE))
+    return fail(OGN_EINVAL, "ogn_spmm_csr: null pointer");
   if (nnz > 0 && (!col || !mat || n == 0))
     return fail(OGN_EINVAL, "ogn_spmm_csr: nnz > 0 needs col, mat and n > 0");
   if (value && value_width != 1 && value_width != k)
@@ -65,11 +96,12 @@ int ogn_spmm_csr(const void* rowptr, const void* col, int index_dtype, const voi
   p.k = k;
   p.nnz_bound = nnz;
   p.reduce = reduce;
-  p.mm_mode = MM_SPMM;
+  p.val_op = message_op;
+  p.mm_mode = semantics == OGN_SPMM_DGL ? MM_NANPROP : MM_SPMM;
   p.seed_mode = SEED_NONE;
   p.arg_empty = nnz;
   return run(pl, p, in_dtype, index_dtype, true, mm ? RK_MINMAX : RK_SUM, batch, workspace,
              workspace_bytes, static_cast<hipStream_t>(stream), "spmm");
 }
 
-}  // extern "C"
+

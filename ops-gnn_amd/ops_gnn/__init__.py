@@ -24,6 +24,8 @@ from .scatter import (
     scatter, scatter_sum, scatter_add, scatter_mul, scatter_mean, scatter_min, scatter_max,
 )
 from .softmax import scatter_softmax, scatter_log_softmax, scatter_logsumexp
+from .sddmm_csr import sddmm_csr
+from .spmm import spmm, bspmm
 
 __version__ = "0.1.0"
 
@@ -44,4 +46,5 @@ __all__ = [
     "segment_max_coo", "segment_logsumexp",
     "scatter", "scatter_sum", "scatter_add", "scatter_mul", "scatter_mean", "scatter_min", "scatter_max",
     "scatter_softmax", "scatter_log_softmax", "scatter_logsumexp",
+    "sddmm_csr", "spmm", "bspmm",
 ]

@@ -56,6 +56,11 @@ SIGNATURES = {
     "ogn_spmm_csr_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _int, _int]),
     "ogn_spmm_csr": (_int, [_vp, _vp, _int, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _i64,
                             _vp, _int, _vp, _int, _vp, _sz, _vp]),
+    "ogn_spmm_csr_ex": (_int, [_vp, _vp, _int, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _i64,
+                               _vp, _int, _vp, _int, _int, _int, _vp, _sz, _vp]),
+    "ogn_sddmm_csr_workspace_size": (_sz, [_i64, _i64, _int]),
+    "ogn_sddmm_csr": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _i64, _int, _vp, _i64, _int, _i64, _int, _int,
+                             _vp, _vp, _sz, _vp]),
     "ogn_ind2ptr": (_int, [_vp, _int, _i64, _i64, _vp, _vp]),
     "ogn_ptr2ind": (_int, [_vp, _int, _i64, _i64, _vp, _vp]),
     "ogn_segment_reduce_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _int, _int]),
@@ -75,7 +80,10 @@ SIGNATURES = {
 
 # reduce / semantics codes (include/ogn.h)
 R_SUM, R_MEAN, R_MIN, R_MAX, R_PROD, R_LSE = range(6)
-SEM_SEGMENT_CSR, SEM_SEGMENT_COO, SEM_SCATTER = range(3)
+SEM_SEGMENT_CSR, SEM_SEGMENT_COO, SEM_SCATTER, SEM_DGL = range(4)
+MSG_MUL, MSG_ADD, MSG_SUB, MSG_DIV = range(4)
+SPMM_TORCH_SPARSE, SPMM_DGL = range(2)
+SDDMM_OPS = {"dot": 0, "add": 1, "sub": 2, "mul": 3, "div": 4, "copy_lhs": 5, "copy_rhs": 6}
 SEG_HAS_OUT = 1
 
 for _name, (_res, _args) in SIGNATURES.items():

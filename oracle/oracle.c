@@ -357,3 +357,80 @@ void oracle_group_softmax(const float* src, const int64_t* index, int64_t before
   free(pos);
   free(fill);
 }
+
+/* ---------------------------------------------------------------- SDDMM
+ * reference test/sddmm_csr/arch22/golden.py:18-90: per edge e with row r
+ * (ptr[r] <= e < ptr[r+1]) and column col[e], the operands are
+ * lhs[t_l(e)] / rhs[t_r(e)] with t = 0 -> r, 1 -> e, 2 -> col[e].
+ * op 0 dot (sum over k, double), 1 add, 2 sub, 3 mul, 4 div, 5 copy_lhs,
+ * 6 copy_rhs.  out: [nnz] for dot, [nnz, k] otherwise.
+ */
+void oracle_sddmm(const int64_t* ptr, const int64_t* col, int64_t m, const float* lhs, const float* rhs,
+                  int lt, int rt, int op, int64_t k, double* out) {
+  for (int64_t r = 0; r < m; ++r) {
+    for (int64_t e = ptr[r]; e < ptr[r + 1]; ++e) {
+      const int64_t li = lt == 0 ? r : (lt == 1 ? e : col[e]);
+      const int64_t ri = rt == 0 ? r : (rt == 1 ? e : col[e]);
+      if (op == 0) {
+        double s = 0.0;
+        for (int64_t j = 0; j < k; ++j) s += (double)lhs[li * k + j] * (double)rhs[ri * k + j];
+        out[e] = s;
+        continue;
+      }
+      for (int64_t j = 0; j < k; ++j) {
+        const double a = op == 6 ? 0.0 : (double)lhs[li * k + j];
+        const double b = op == 5 ? 0.0 : (double)rhs[ri * k + j];
+        double v;
+        switch (op) {
+          case 1: v = a + b; break;
+          case 2: v = a - b; break;
+          case 3: v = a * b; break;
+          case 4: v = a / b; break;
+          case 5: v = a; break;
+          default: v = b; break;
+        }
+        out[e * k + j] = v;
+      }
+    }
+  }
+}
+
+/* ---------------------------------------------------------------- DGL spmm
+ * reference test/unified_spmm/arch22/golden.py:13-92 (messages, then
+ * index_add for sum/mean and scatter_reduce amax/amin with include_self from
+ * -inf/+inf for max/min, empty rows -> 0).  torch's amax/amin propagate NaN,
+ * so a row holding a NaN message is NaN.  msg: 0 copy (x), 1 add, 2 sub,
+ * 3 mul, 4 div with w[e, (j | 0)] (width 1 or k); w may be NULL for copy.
+ * copy_rhs is msg 5 (the edge value itself, x unused).
+ * reduce: 0 sum, 1 mean, 2 min, 3 max.
+ */
+void oracle_spmm_dgl(const int64_t* ptr, const int64_t* col, int64_t m, const float* x, const float* w,
+                     int64_t width, int msg, int reduce, int64_t k, double* out) {
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int64_t r = 0; r < m; ++r) {
+    for (int64_t j = 0; j < k; ++j) {
+      const int64_t a = ptr[r], z = ptr[r + 1];
+      double acc = reduce == 2 ? INFINITY : (reduce == 3 ? -INFINITY : 0.0);
+      int nan = 0;
+      for (int64_t e = a; e < z; ++e) {
+        const double xv = msg == 5 ? 0.0 : (double)x[col[e] * k + j];
+        const double wv = w ? (double)w[width == 1 ? e : e * k + j] : 0.0;
+        double v;
+        switch (msg) {
+          case 1: v = xv + wv; break;
+          case 2: v = xv - wv; break;
+          case 3: v = xv * wv; break;
+          case 4: v = xv / wv; break;
+          case 5: v = wv; break;
+          default: v = xv; break;
+        }
+        if (reduce <= 1) acc += v;
+        else if (isnan(v)) nan = 1;
+        else if (reduce == 2 ? v < acc : v > acc) acc = v;
+      }
+      if (reduce == 1 && z > a) acc /= (double)(z - a);
+      if (reduce >= 2) acc = (z == a) ? 0.0 : (nan ? NAN : acc);
+      out[r * k + j] = acc;
+    }
+  }
+}

@@ -54,6 +54,9 @@ def lib():
                                      ctypes.c_double, _f64p, vp]
         l.oracle_segment_lse.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, _f64p]
         l.oracle_group_softmax.argtypes = [_f32p, _i64p, i64, i64, i64, i64, ctypes.c_int, _f64p]
+        l.oracle_sddmm.argtypes = [_i64p, _i64p, i64, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, i64,
+                                   _f64p]
+        l.oracle_spmm_dgl.argtypes = [_i64p, _i64p, i64, vp, vp, i64, ctypes.c_int, ctypes.c_int, i64, _f64p]
         _lib = l
     return _lib
 
@@ -223,6 +226,53 @@ def group_softmax(src, index, dim, groups, mode):
     shape = src.shape if m < 2 else src.shape[:dim] + (groups,) + src.shape[dim + 1:]
     out = np.zeros(shape, np.float64)
     lib().oracle_group_softmax(np.ascontiguousarray(src.reshape(-1)), idx, before, length, after, groups, m, out)
+    return out
+
+
+SDDMM_OPS = {"dot": 0, "add": 1, "sub": 2, "mul": 3, "div": 4, "copy_lhs": 5, "copy_rhs": 6}
+
+
+def sddmm(ptr, col, lhs, rhs, op="dot", lhs_target=0, rhs_target=2):
+    """reference test/sddmm_csr/arch22/golden.py:74-90; operands [rows, k]
+    (1-D operands are [rows, 1]).  Returns float64 [nnz] (dot) or [nnz, k]."""
+    ptr = _np(ptr, np.int64)
+    col = _np(col, np.int64)
+    l = None if lhs is None else _np(lhs, np.float32)
+    r = None if rhs is None else _np(rhs, np.float32)
+    feat = l if l is not None else r
+    k = 1 if feat.ndim == 1 else feat.shape[1]
+    nnz = col.shape[0]
+    code = SDDMM_OPS[op]
+    out = np.zeros((nnz,) if code == 0 else (nnz, k), np.float64)
+    lib().oracle_sddmm(ptr, col, ptr.shape[0] - 1, _ptr(l), _ptr(r), lhs_target, rhs_target, code, k, out)
+    return out
+
+
+DGL_MSG = {"copy_lhs": 0, "add": 1, "sub": 2, "mul": 3, "div": 4, "copy_rhs": 5}
+
+
+def spmm_dgl(ptr, col, x, rhs, op, reduce):
+    """DGL-style aggregation (reference test/unified_spmm/arch22/golden.py:13-92).
+
+    x [N, k] (None for copy_rhs); rhs [E], [E, 1] or [E, k] (None for copy_lhs).
+    Returns float64 [M, k]."""
+    ptr = _np(ptr, np.int64)
+    col = _np(col, np.int64)
+    xs = None if x is None else _np(x, np.float32)
+    w = None if rhs is None else _np(rhs, np.float32)
+    nnz = col.shape[0]
+    if xs is not None:
+        k = int(np.prod(xs.shape[1:])) if xs.ndim > 1 else 1
+        xs = np.ascontiguousarray(xs.reshape(xs.shape[0], k))
+    else:
+        k = int(np.prod(w.shape[1:])) if w.ndim > 1 else 1
+    width = 0
+    if w is not None:
+        width = int(np.prod(w.shape[1:])) if w.ndim > 1 else 1
+        w = np.ascontiguousarray(w.reshape(nnz, width))
+    m = ptr.shape[0] - 1
+    out = np.zeros((m, k), np.float64)
+    lib().oracle_spmm_dgl(ptr, col, m, _ptr(xs), _ptr(w), width, DGL_MSG[op], REDUCE[reduce], k, out)
     return out
 
 

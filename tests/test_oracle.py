@@ -398,3 +398,85 @@ def test_group_softmax_special_values_follow_torch():
         ref = np.concatenate([fn(t[2 * g:2 * g + 2], 0).numpy() for g in range(4)])
         np.testing.assert_array_equal(np.isnan(out), np.isnan(ref))
         np.testing.assert_allclose(out[~np.isnan(ref)], ref[~np.isnan(ref)])
+
+
+# ----------------------------------------------------------------- SDDMM
+def _csr_small(rng, m, n, avg):
+    deg = rng.poisson(avg, size=m)
+    deg[::5] = 0
+    col = np.concatenate([np.sort(rng.integers(0, n, d)) for d in deg]).astype(np.int64)
+    return np.concatenate([[0], np.cumsum(deg)]).astype(np.int64), col
+
+
+def test_sddmm_dot_matches_sampled_addmm():
+    rng = np.random.default_rng(61)
+    ptr, col = _csr_small(rng, 40, 30, 5)
+    q = rng.standard_normal((40, 8)).astype(np.float32)
+    k = rng.standard_normal((30, 8)).astype(np.float32)
+    got = orc.sddmm(ptr, col, q, k, "dot", 0, 2)
+    a = torch.sparse_csr_tensor(torch.from_numpy(ptr), torch.from_numpy(col), torch.zeros(col.size, dtype=torch.float64),
+                                size=(40, 30))
+    ref = torch.sparse.sampled_addmm(a, torch.from_numpy(q).double(), torch.from_numpy(k).double().t()).values()
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("op", ["dot", "add", "sub", "mul", "div", "copy_lhs", "copy_rhs"])
+@pytest.mark.parametrize("lt,rt", [(0, 2), (2, 0), (1, 0), (2, 1)])
+def test_sddmm_brute_force(op, lt, rt):
+    rng = np.random.default_rng(62)
+    ptr, col = _csr_small(rng, 12, 10, 3)
+    nnz = col.size
+    rows = {0: 12, 1: nnz, 2: 10}
+    lhs = rng.standard_normal((rows[lt], 3)).astype(np.float32)
+    rhs = (rng.standard_normal((rows[rt], 3)) + 3).astype(np.float32)
+    got = orc.sddmm(ptr, col, lhs if op != "copy_rhs" else None, rhs if op != "copy_lhs" else None, op, lt, rt)
+    for r in range(12):
+        for e in range(ptr[r], ptr[r + 1]):
+            pick = lambda t: r if t == 0 else (e if t == 1 else col[e])
+            a = lhs[pick(lt)].astype(np.float64)
+            b = rhs[pick(rt)].astype(np.float64)
+            ref = {"dot": (a * b).sum(), "add": a + b, "sub": a - b, "mul": a * b, "div": a / b,
+                   "copy_lhs": a, "copy_rhs": b}[op]
+            np.testing.assert_allclose(got[e], ref, rtol=1e-12)
+
+
+# ----------------------------------------------------------------- DGL spmm
+@pytest.mark.parametrize("reduce,torch_reduce", [("max", "amax"), ("min", "amin")])
+def test_spmm_dgl_extrema_propagate_nan_like_scatter_reduce(reduce, torch_reduce):
+    rng = np.random.default_rng(63)
+    ptr, col = _csr_small(rng, 30, 20, 4)
+    x = rng.standard_normal((20, 6)).astype(np.float32)
+    x[rng.random(x.shape) < 0.05] = np.nan
+    got = orc.spmm_dgl(ptr, col, x, None, "copy_lhs", reduce)
+    rows = torch.repeat_interleave(torch.arange(30), torch.from_numpy(np.diff(ptr)))
+    init = float("-inf") if reduce == "max" else float("inf")
+    ref = torch.full((30, 6), init, dtype=torch.float64).scatter_reduce(
+        0, rows[:, None].expand(-1, 6), torch.from_numpy(x).double()[torch.from_numpy(col)], torch_reduce,
+        include_self=True)
+    ref[torch.from_numpy(np.diff(ptr)) == 0] = 0
+    np.testing.assert_array_equal(np.isnan(got), torch.isnan(ref).numpy())
+    np.testing.assert_allclose(got, ref.numpy(), equal_nan=True)
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "copy_rhs"])
+@pytest.mark.parametrize("width", [1, 4])
+def test_spmm_dgl_messages_brute_force(op, width):
+    rng = np.random.default_rng(64)
+    ptr, col = _csr_small(rng, 15, 9, 3)
+    x = rng.standard_normal((9, 4)).astype(np.float32)
+    w = (rng.standard_normal((col.size, width)) + 2).astype(np.float32)
+    for reduce in ("sum", "mean", "max"):
+        got = orc.spmm_dgl(ptr, col, None if op == "copy_rhs" else x, w if width == 4 or op != "copy_rhs" else
+                           np.repeat(w, 4, axis=1), op, reduce)
+        for r in range(15):
+            msgs = []
+            for e in range(ptr[r], ptr[r + 1]):
+                a = x[col[e]].astype(np.float64)
+                b = np.broadcast_to(w[e].astype(np.float64), (4,))
+                msgs.append({"add": a + b, "sub": a - b, "mul": a * b, "div": a / b, "copy_rhs": b}[op])
+            if not msgs:
+                ref = np.zeros(4)
+            else:
+                arr = np.stack(msgs)
+                ref = {"sum": arr.sum(0), "mean": arr.mean(0), "max": arr.max(0)}[reduce]
+            np.testing.assert_allclose(got[r], ref, rtol=1e-12, atol=1e-12)
