@@ -222,7 +222,11 @@ __global__ __launch_bounds__(256) void chunk_rows_kernel(Params p) {
   for (int64_t c = c0; c <= c1; ++c) cr[c] = r;
 }
 
-template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER>
+// FAST instances fix the common case at compile time -- messages x * w with
+// at most one weight per position, no product reduction, and the first-tie /
+// NaN-ignoring extremum rules -- which keeps the per-lane state small enough
+// for 6-7 waves per SIMD (the generic instance needs about twice the VGPRs).
+template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER, bool FAST>
 __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
   using E = Elem<DT>;
   using S_t = typename E::S;
@@ -247,10 +251,12 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
   const S_t* __restrict__ srcb = static_cast<const S_t*>(p.src) + b * p.src_bstride;
   const S_t* __restrict__ val = static_cast<const S_t*>(p.val);
   const bool is_min = p.reduce == OGN_REDUCE_MIN;
-  const bool is_prod = p.reduce == OGN_REDUCE_PROD;
-  const bool later = p.mm_mode == MM_LATER;
-  const bool nanprop = p.mm_mode == MM_NANPROP;
-  const int vop = p.val_op;
+  const bool is_prod = !FAST && p.reduce == OGN_REDUCE_PROD;
+  const bool later = !FAST && p.mm_mode == MM_LATER;
+  const bool nanprop = !FAST && p.mm_mode == MM_NANPROP;
+  const int vop = FAST ? (int)OP_MUL : p.val_op;
+  const int val_mode = FAST ? std::min(p.val_mode, 1) : p.val_mode;
+  constexpr int NW = (VL && !FAST) ? NE : 1;  // weights held per step
 
   const int64_t base = ptr[0];
   const int64_t end = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[M] - base, p.nnz_bound), 0);
@@ -386,59 +392,85 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
     }
     cl = std::min<int64_t>(std::max<int64_t>(cl, 0), p.n - 1);
     float vl = 1.f;
-    if (p.val_mode == 1) vl = ev ? E::load1(val, el) : 0.f;
+    if (val_mode == 1) vl = ev ? E::load1(val, el) : 0.f;
     const int nw = (int)std::min<int64_t>(kWave, hi - wbase);
     const int nsteps = (nw + S - 1) / S;
     for (int j0 = 0; j0 < nsteps; j0 += kUnroll) {
-      float x[kUnroll][NE];
-      float w[kUnroll][VL ? NE : 1];
+      // Raw 16-byte loads are kept as issued and unpacked when consumed, so
+      // 16-bit features occupy half the registers and no load is waited for
+      // before the last one has been issued.
+      uint4 xr[kUnroll];
+      float xs[kUnroll];
+      float w[kUnroll][NW];
+      // Phase 1: every lane shuffle of the U steps (positions and weights).
+      // Doing them before any gather is issued keeps the wait for the staged
+      // col/value loads ahead of the gathers, so the U gathers overlap.
+      int64_t cc[kUnroll];
+      float ws[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int idx = (j0 + u) * S + sub;
-        int64_t cc;
         if constexpr (GATHER) {
-          cc = (int64_t)shfl64((IDX)cl, idx & (kWave - 1));
+          cc[u] = (int64_t)shfl64((IDX)cl, idx & (kWave - 1));
         } else {
-          cc = std::min<int64_t>(wbase + idx, p.n - 1);
+          cc[u] = std::min<int64_t>(wbase + idx, p.n - 1);
         }
-        const float ws = p.val_mode == 1 ? shflf(vl, idx & (kWave - 1)) : 1.f;
+        ws[u] = shflf(vl, idx & (kWave - 1));
+      }
+      // Phase 2: issue the U gathers back to back.
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int idx = (j0 + u) * S + sub;
         const bool ok = (j0 + u) < nsteps && idx < nw && kok;
         if constexpr (VL) {
-          if (ok) {
-            E::unpack(load16(srcb + cc * K + k0), x[u]);
-          } else {
+          xr[u] = ok ? load16(srcb + cc[u] * K + k0) : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-            for (int i = 0; i < NE; ++i) x[u][i] = 0.f;
-          }
+          for (int i = 0; i < NW; ++i) w[u][i] = ws[u];
+          if constexpr (NW > 1) {
+            if (val_mode == 2 && ok) {
+              float wv[NE];
+              E::unpack(load16(val + (wbase + idx) * K + k0), wv);
 #pragma unroll
-          for (int i = 0; i < NE; ++i) w[u][i] = ws;
-          if (p.val_mode == 2 && ok) {
-            float wv[NE];
-            E::unpack(load16(val + (wbase + idx) * K + k0), wv);
-#pragma unroll
-            for (int i = 0; i < NE; ++i) w[u][i] = wv[i];
+              for (int i = 0; i < NE; ++i) w[u][i] = wv[i];
+            }
           }
         } else {
-          x[u][0] = ok ? E::load1(srcb, cc * K + k0) : 0.f;
-          w[u][0] = ws;
-          if (p.val_mode == 2 && ok) w[u][0] = E::load1(val, (wbase + idx) * K + k0);
+          xs[u] = ok ? E::load1(srcb, cc[u] * K + k0) : 0.f;
+          w[u][0] = ws[u];
+          if (val_mode == 2 && ok) w[u][0] = E::load1(val, (wbase + idx) * K + k0);
         }
       }
-#pragma unroll
+      // Phase 3: consume the steps in order.  The loop is not unrolled (the
+      // row-finishing code it contains is large); the staged steps rotate
+      // down one slot per iteration so that they stay in registers.
+#pragma unroll 1
       for (int u = 0; u < kUnroll; ++u) {
         if (j0 + u >= nsteps) break;
         const int64_t e_first = wbase + (int64_t)(j0 + u) * S;
         const int64_t last = std::min<int64_t>(e_first + S, hi) - 1;
         const int64_t e_mine = e_first + sub;
         const bool valid = e_mine < hi;
+        float x[NE];
+        if constexpr (VL) E::unpack(xr[0], x);
+        else x[0] = xs[0];
+        float wcur[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) wcur[i] = w[0][i];
+#pragma unroll
+        for (int t = 0; t + 1 < kUnroll; ++t) {
+          xr[t] = xr[t + 1];
+          xs[t] = xs[t + 1];
+#pragma unroll
+          for (int i = 0; i < NW; ++i) w[t][i] = w[t + 1][i];
+        }
         bool added = false;
         while (true) {
           if (!added && valid && e_mine < re) {
 #pragma unroll
             for (int i = 0; i < NE; ++i) {
-              const float wi = w[u][VL ? i : 0];
+              const float wi = wcur[NW > 1 ? i : 0];
               if constexpr (RK == RK_MINMAX) {
-                const MT pv = apply_op<MT>((MT)x[u][i], (MT)wi, vop);
+                const MT pv = apply_op<MT>((MT)x[i], (MT)wi, vop);
                 if (nanprop) {
                   if (barg[i] == kNone || (pv != pv) || better(pv, best[i], is_min)) {
                     best[i] = pv;
@@ -454,14 +486,14 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
                 }
               } else if constexpr (RK == RK_LSE) {
                 float m = (float)best[i];
-                lse_add(m, acc[i], apply_op<float>(x[u][i], wi, vop));
+                lse_add(m, acc[i], apply_op<float>(x[i], wi, vop));
                 best[i] = m;
               } else {
                 if (vop == OP_MUL)
-                  acc[i] = is_prod ? acc[i] * (x[u][i] * wi) : __builtin_fmaf(x[u][i], wi, acc[i]);
+                  acc[i] = is_prod ? acc[i] * (x[i] * wi) : __builtin_fmaf(x[i], wi, acc[i]);
                 else
-                  acc[i] = is_prod ? acc[i] * apply_op<float>(x[u][i], wi, vop)
-                                   : acc[i] + apply_op<float>(x[u][i], wi, vop);
+                  acc[i] = is_prod ? acc[i] * apply_op<float>(x[i], wi, vop)
+                                   : acc[i] + apply_op<float>(x[i], wi, vop);
               }
             }
             added = true;
@@ -616,26 +648,41 @@ OGN_ENGINE_DECL(launch_contig_f16)
 OGN_ENGINE_DECL(launch_contig_bf16)
 #undef OGN_ENGINE_DECL
 
-template <int DT, typename IDX, bool VL, int RK, bool GATHER>
+template <int DT, typename IDX, bool VL, int RK, bool GATHER, bool FAST>
 void launch_g(int g, dim3 grid, hipStream_t s, const Params& p) {
   switch (g) {
 #define OGN_G(GV) \
-  case GV: hipLaunchKernelGGL((engine_kernel<DT, IDX, GV, VL, RK, GATHER>), grid, dim3(kBlock), 0, s, p); break;
+  case GV: hipLaunchKernelGGL((engine_kernel<DT, IDX, GV, VL, RK, GATHER, FAST>), grid, dim3(kBlock), 0, s, p); break;
     OGN_G(1) OGN_G(2) OGN_G(4) OGN_G(8) OGN_G(16) OGN_G(32) OGN_G(64)
 #undef OGN_G
     default: break;
   }
 }
 
+template <int DT, typename IDX, int RK, bool GATHER, bool FAST>
+void launch_rk_f(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
+  if (pl.vec) {
+    launch_g<DT, IDX, true, RK, GATHER, FAST>(pl.g, grid, s, p);
+  } else if (pl.g == 1) {
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 1, false, RK, GATHER, FAST>), grid, dim3(kBlock), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 64, false, RK, GATHER, FAST>), grid, dim3(kBlock), 0, s, p);
+  }
+}
+
+// The FAST instance covers requests whose messages are x * w with a scalar
+// (or no) weight, that do not multiply, and whose extremum rule is first-tie
+// with NaN ignored (torch_sparse SpMM, segment_csr).
+inline bool fast_ok(int rk, const Params& p) {
+  if (p.val_op != OP_MUL || p.val_mode == 2 || p.reduce == OGN_REDUCE_PROD) return false;
+  if (rk == RK_MINMAX) return p.mm_mode == MM_SPMM || p.mm_mode == MM_SEGCSR;
+  return true;
+}
+
 template <int DT, typename IDX, int RK, bool GATHER>
 void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
-  if (pl.vec) {
-    launch_g<DT, IDX, true, RK, GATHER>(pl.g, grid, s, p);
-  } else if (pl.g == 1) {
-    hipLaunchKernelGGL((engine_kernel<DT, IDX, 1, false, RK, GATHER>), grid, dim3(kBlock), 0, s, p);
-  } else {
-    hipLaunchKernelGGL((engine_kernel<DT, IDX, 64, false, RK, GATHER>), grid, dim3(kBlock), 0, s, p);
-  }
+  if (fast_ok(RK, p)) launch_rk_f<DT, IDX, RK, GATHER, true>(pl, grid, s, p);
+  else launch_rk_f<DT, IDX, RK, GATHER, false>(pl, grid, s, p);
 }
 
 // Gather mode (SpMM) instantiates int32 and int64 indices with sum / min-max;
