@@ -279,6 +279,24 @@ int ogn_group_softmax_apply(const void* src, int dtype, const void* index, int i
                             void* out, int log_softmax, void* stream);
 int ogn_group_lse_from_stats(const float* m, const float* s, int64_t cells, void* out, int dtype, void* stream);
 
+/* Backward of the grouped softmax family (reference RunBackward,
+ * csrc/npu/scatter_softmax/common/grouped_softmax_shared.h:212-250 and
+ * csrc/npu/scatter_logsumexp/common/grouped_logsumexp_shared.h:92-136; Python
+ * python/ops_gnn/_grouped_softmax.py:122-133, scatter_logsumexp.py:78-84).
+ *  mode 0 softmax:     grad_src = out * (g - T),      T = group sum of out * g
+ *  mode 1 log_softmax: grad_src = g - exp(out) * T,   T = group sum of g
+ *    saved = forward output, grad = its gradient, both [before, len, after];
+ *    workspace: before * groups * after fp32 (cleared by the call).
+ *  mode 2 logsumexp:   grad_src = g[group] * exp(x - out[group])
+ *    saved = forward src [before, len, after], reduced = forward output and
+ *    grad = its gradient, both [before, groups, after]; no workspace.
+ * Positions whose index is outside [0, groups) get 0.  fp32 math; group sums
+ * use atomics (one per run of equal targets in a wavefront). */
+int ogn_group_softmax_backward(const void* saved, const void* grad, const void* reduced, int dtype,
+                               const void* index, int index_dtype, int64_t before, int64_t len, int64_t after,
+                               int64_t groups, int mode, void* grad_src, float* workspace, size_t workspace_bytes,
+                               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

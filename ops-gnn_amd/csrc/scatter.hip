@@ -245,6 +245,102 @@ __global__ __launch_bounds__(256) void group_lse_kernel(GroupArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ grouped softmax backward
+// softmax:     grad_src = out * (g - T[group]),        T = sum over the group of out * g
+// log_softmax: grad_src = g - exp(out) * T[group],     T = sum over the group of g
+// logsumexp:   grad_src = g_red[group] * exp(x - out_red[group])   (no group sum)
+// Positions whose index is outside [0, groups) get 0.
+struct GroupBwdArgs {
+  const void* saved;  // softmax / log_softmax: forward output; logsumexp: src
+  const void* grad;   // grad of the forward output (same shape as saved; [b, groups, f] for logsumexp)
+  const void* red;    // logsumexp: the forward output [b, groups, f]
+  int dt;
+  const void* index;
+  int idx64;
+  int64_t before, len, after, groups;
+  float* total;  // [b, groups, f] fp32 group sums (zeroed by the caller of the sum pass)
+  void* grad_src;
+  int mode;  // 0 softmax, 1 log_softmax, 2 logsumexp
+};
+
+__device__ __forceinline__ int64_t bwd_group_of(const GroupBwdArgs& a, int64_t l) {
+  return a.idx64 ? static_cast<const int64_t*>(a.index)[l] : (int64_t) static_cast<const int32_t*>(a.index)[l];
+}
+
+__global__ __launch_bounds__(256) void group_zero_kernel(float* t, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) t[i] = 0.f;
+}
+
+// Group sums with one atomic per run of equal targets inside a wavefront:
+// a segmented inclusive scan over the 64 lanes (runs are found from the
+// neighbour's target, so any index order is correct) leaves each run's sum
+// in its last lane.  With a sorted index and after == 1 a wave issues about
+// one atomic per group it touches instead of one per element.
+__global__ __launch_bounds__(256) void group_bwd_sum_kernel(GroupBwdArgs a) {
+  const int64_t total = a.before * a.len * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int lane = lane_id();
+  for (int64_t base = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1)); base < total;
+       base += stride) {
+    const int64_t i = base + lane;
+    int64_t key = -1;
+    float v = 0.f;
+    if (i < total) {
+      const int64_t f = i % a.after;
+      const int64_t l = (i / a.after) % a.len;
+      const int64_t b = i / (a.after * a.len);
+      const int64_t g = bwd_group_of(a, l);
+      if (g >= 0 && g < a.groups) {
+        key = (b * a.groups + g) * a.after + f;
+        const float gv = load_float(a.grad, a.dt, i);
+        v = a.mode == 0 ? load_float(a.saved, a.dt, i) * gv : gv;
+      }
+    }
+    const int64_t prev = shfl64(key, lane > 0 ? lane - 1 : 0);
+    const int head = (lane == 0 || prev != key) ? lane : 0;
+    // start lane of this lane's run = max of the head marks up to this lane
+    int start = head;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int o = shfl32(start, lane >= off ? lane - off : lane);
+      if (lane >= off) start = start > o ? start : o;
+    }
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const float o = shflf(v, lane >= off ? lane - off : lane);
+      if (lane - off >= start) v += o;
+    }
+    const int64_t next = shfl64(key, lane < kWave - 1 ? lane + 1 : lane);
+    const bool tail = lane == kWave - 1 || next != key;
+    if (tail && key >= 0) atomicAdd(&a.total[key], v);
+  }
+}
+
+__global__ __launch_bounds__(256) void group_bwd_apply_kernel(GroupBwdArgs a) {
+  const int64_t total = a.before * a.len * a.after;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t f = i % a.after;
+    const int64_t l = (i / a.after) % a.len;
+    const int64_t b = i / (a.after * a.len);
+    const int64_t g = bwd_group_of(a, l);
+    float v = 0.f;
+    if (g >= 0 && g < a.groups) {
+      const int64_t o = (b * a.groups + g) * a.after + f;
+      if (a.mode == 2) {
+        const float x = load_float(a.saved, a.dt, i);
+        v = load_float(a.grad, a.dt, o) * expf(x - load_float(a.red, a.dt, o));
+      } else {
+        const float y = load_float(a.saved, a.dt, i);
+        const float gv = load_float(a.grad, a.dt, i);
+        v = a.mode == 0 ? y * (gv - a.total[o]) : gv - expf(y) * a.total[o];
+      }
+    }
+    store_floats<1>(a.grad_src, a.dt, i, &v);
+  }
+}
+
 unsigned grid_for(int64_t total) {
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, 65536));
 }
@@ -405,6 +501,51 @@ int ogn_group_lse_from_stats(const float* m, const float* s, int64_t cells, void
   TimedLaunch t("group_lse", st);
   hipLaunchKernelGGL(group_lse_kernel, dim3(grid_for(cells)), dim3(256), 0, st, a);
   return check_launch("ogn_group_lse_from_stats");
+}
+
+int ogn_group_softmax_backward(const void* saved, const void* grad, const void* reduced, int dtype,
+                               const void* index, int index_dtype, int64_t before, int64_t len, int64_t after,
+                               int64_t groups, int mode, void* grad_src, float* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (before < 0 || len < 0 || after < 0 || groups < 0)
+    return fail(OGN_EINVAL, "ogn_group_softmax_backward: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_group_softmax_backward: dtype must be float32, float16 or bfloat16");
+  if (index_dtype != OGN_I32 && index_dtype != OGN_I64)
+    return fail(OGN_EINVAL, "ogn_group_softmax_backward: index dtype must be int32 or int64");
+  if (mode < 0 || mode > 2) return fail(OGN_EINVAL, "ogn_group_softmax_backward: mode must be 0, 1 or 2");
+  const int64_t total = before * len * after;
+  if (total == 0) return OGN_OK;
+  const int64_t cells = before * groups * after;
+  if (!saved || !grad || !index || !grad_src || (mode == 2 && !reduced))
+    return fail(OGN_EINVAL, "ogn_group_softmax_backward: null pointer");
+  if (mode != 2 && cells > 0 && (!workspace || workspace_bytes < (size_t)cells * sizeof(float)))
+    return fail(OGN_EINVAL, "ogn_group_softmax_backward: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  GroupBwdArgs a{};
+  a.saved = saved;
+  a.grad = grad;
+  a.red = reduced;
+  a.dt = dtype;
+  a.index = index;
+  a.idx64 = index_dtype == OGN_I64;
+  a.before = before;
+  a.len = len;
+  a.after = after;
+  a.groups = groups;
+  a.total = workspace;
+  a.grad_src = grad_src;
+  a.mode = mode;
+  if (mode != 2 && cells > 0) {
+    TimedLaunch t("group_bwd_sum", st);
+    hipLaunchKernelGGL(group_zero_kernel, dim3(grid_for(cells)), dim3(256), 0, st, workspace, cells);
+    hipLaunchKernelGGL(group_bwd_sum_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);
+  }
+  {
+    TimedLaunch t("group_bwd_apply", st);
+    hipLaunchKernelGGL(group_bwd_apply_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);
+  }
+  return check_launch("ogn_group_softmax_backward");
 }
 
 }  // extern "C"

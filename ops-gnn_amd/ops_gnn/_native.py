@@ -239,3 +239,23 @@ def group_lse_from_stats(m, s, dtype) -> torch.Tensor:
     check(lib.ogn_group_lse_from_stats(dptr(m), dptr(s), m.numel(), dptr(out), _lib.TORCH_TO_OGN[dtype],
                                        stream_of(m)), "group logsumexp")
     return out
+
+
+def group_softmax_backward(saved3, grad3, index, groups, mode, reduced3=None) -> torch.Tensor:
+    """Gradient of the grouped softmax family w.r.t. src ([B, L, F] like saved3).
+
+    mode 0 softmax / 1 log_softmax: saved3 = forward output, grad3 = its grad.
+    mode 2 logsumexp: saved3 = forward src, reduced3 = forward output
+    [B, groups, F], grad3 = its grad (same shape as reduced3)."""
+    b, length, f = saved3.shape
+    out = torch.empty_like(saved3)
+    if out.numel() == 0:
+        return out
+    idx = index.contiguous()
+    cells = b * groups * f if mode != 2 else 0
+    ws = torch.empty(max(cells, 1), dtype=torch.float32, device=saved3.device)
+    rc = lib.ogn_group_softmax_backward(dptr(saved3), dptr(grad3), dptr(reduced3), _lib.TORCH_TO_OGN[saved3.dtype],
+                                        dptr(idx), _index_code(idx), b, length, f, groups, mode, dptr(out),
+                                        dptr(ws), ws.numel() * 4, stream_of(saved3))
+    check(rc, "group softmax backward")
+    return out

@@ -12,6 +12,10 @@ s = sum(exp(x - clamp(m))) -- from the contiguous-segment engine when the
 index is sorted (deterministic), from atomics otherwise -- then one
 elementwise pass (softmax / log_softmax) or one pass over the groups
 (logsumexp).  fp32 math for every dtype.
+
+Backward (reference python/ops_gnn/_grouped_softmax.py:102-133,
+scatter_logsumexp.py:57-84), all HIP: softmax out * (g - sum_group(out * g)),
+log_softmax g - exp(out) * sum_group(g), logsumexp g[group] * exp(x - out[group]).
 """
 
 from typing import Optional
@@ -91,14 +95,59 @@ def _stats(src3, index, groups, is_sorted):
     return _native.group_stats(src3, index, groups, is_sorted)
 
 
+class _GroupedSoftmax(torch.autograd.Function):
+    """softmax / log_softmax over index groups with the analytic grouped Jacobian."""
+
+    @staticmethod
+    def forward(ctx, src, index, groups, is_sorted, log_softmax, shape3):
+        src3 = src.contiguous().reshape(shape3)
+        m, s = _stats(src3, index, groups, is_sorted)
+        out3 = _native.group_softmax_apply(src3, index, groups, m, s, log_softmax)
+        ctx.save_for_backward(out3, index)
+        ctx.groups, ctx.log_softmax, ctx.shape3 = groups, log_softmax, src3.shape
+        return out3.reshape(src.shape)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad):
+        out3, index = ctx.saved_tensors
+        g3 = grad.to(out3.dtype).contiguous().reshape(ctx.shape3)
+        gsrc = _native.group_softmax_backward(out3, g3, index, ctx.groups, 1 if ctx.log_softmax else 0)
+        return gsrc.reshape(grad.shape), None, None, None, None, None
+
+
+class _GroupedLogSumExp(torch.autograd.Function):
+    """log-sum-exp over index groups; gradient g[group] * exp(x - out[group])."""
+
+    @staticmethod
+    def forward(ctx, src, index, groups, is_sorted, shape3, shape):
+        src3 = src.contiguous().reshape(shape3)
+        if is_sorted:
+            ptr = _native.ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups)
+            res3, _ = _native.segment_reduce(src3, ptr, groups, _lib.R_LSE, _lib.SEM_SEGMENT_CSR)
+        else:
+            m, s = _stats(src3, index, groups, False)
+            res3 = _native.group_lse_from_stats(m, s, src.dtype)
+        ctx.save_for_backward(src3, res3, index)
+        ctx.groups, ctx.src_shape = groups, src.shape
+        return res3.reshape(shape)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad):
+        src3, res3, index = ctx.saved_tensors
+        g3 = grad.to(res3.dtype).contiguous().reshape(res3.shape)
+        gsrc = _native.group_softmax_backward(src3, g3, index, ctx.groups, 2, reduced3=res3)
+        return gsrc.reshape(ctx.src_shape), None, None, None, None, None
+
+
 def scatter_softmax(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
                     dim_size: Optional[int] = None) -> torch.Tensor:
     """Softmax over the groups of ``src`` along ``dim`` defined by ``index``."""
     dim, groups, is_sorted, src3 = _prepare("scatter_softmax", src, index, dim, dim_size)
     if src.numel() == 0:
         return torch.zeros_like(src)
-    m, s = _stats(src3, index, groups, is_sorted)
-    return _native.group_softmax_apply(src3, index, groups, m, s, False).reshape(src.shape)
+    return _GroupedSoftmax.apply(src, index, groups, is_sorted, False, src3.shape)
 
 
 def scatter_log_softmax(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
@@ -107,8 +156,7 @@ def scatter_log_softmax(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
     dim, groups, is_sorted, src3 = _prepare("scatter_log_softmax", src, index, dim, dim_size)
     if src.numel() == 0:
         return torch.zeros_like(src)
-    m, s = _stats(src3, index, groups, is_sorted)
-    return _native.group_softmax_apply(src3, index, groups, m, s, True).reshape(src.shape)
+    return _GroupedSoftmax.apply(src, index, groups, is_sorted, True, src3.shape)
 
 
 def scatter_logsumexp(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
@@ -120,9 +168,4 @@ def scatter_logsumexp(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
     shape[dim] = groups
     if src3.numel() == 0 or groups == 0:
         return torch.full(shape, float("-inf"), dtype=src.dtype, device=src.device)
-    if is_sorted:
-        ptr = _native.ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups)
-        res3, _ = _native.segment_reduce(src3, ptr, groups, _lib.R_LSE, _lib.SEM_SEGMENT_CSR)
-        return res3.reshape(shape)
-    m, s = _stats(src3, index, groups, False)
-    return _native.group_lse_from_stats(m, s, src.dtype).reshape(shape)
+    return _GroupedLogSumExp.apply(src, index, groups, is_sorted, src3.shape, shape)

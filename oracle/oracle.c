@@ -358,6 +358,61 @@ void oracle_group_softmax(const float* src, const int64_t* index, int64_t before
   free(fill);
 }
 
+/* ---------------------------------------------------------------- grouped softmax backward
+ * Gradient of oracle_group_softmax w.r.t. src, computed from the float64
+ * forward -- what autograd of the reference's float64 golden gives
+ * (test/common/grouped_softmax_golden.py:86-98 for logsumexp; softmax and
+ * log_softmax through torch's own Jacobians):
+ *   softmax:     y * (g - sum_group(y * g))
+ *   log_softmax: g - exp(y) * sum_group(g)
+ *   logsumexp:   g[group] * exp(x - lse[group])   (grad is [before, groups, after])
+ * Positions outside every group get 0.
+ */
+void oracle_group_softmax_backward(const float* src, const float* grad, const int64_t* index, int64_t before,
+                                   int64_t len, int64_t after, int64_t groups, int mode, double* gsrc) {
+  const int64_t total = before * len * after;
+  const int64_t ocells = mode == 2 ? before * groups * after : total;
+  double* y = (double*)malloc((size_t)(ocells > 0 ? ocells : 1) * sizeof(double));
+  oracle_group_softmax(src, index, before, len, after, groups, mode, y);
+  for (int64_t i = 0; i < total; ++i) gsrc[i] = 0.0;
+  if (mode == 2) {
+    for (int64_t b = 0; b < before; ++b)
+      for (int64_t l = 0; l < len; ++l) {
+        const int64_t g = index[l];
+        if (g < 0 || g >= groups) continue;
+        for (int64_t f = 0; f < after; ++f) {
+          const int64_t o = (b * groups + g) * after + f, i = (b * len + l) * after + f;
+          gsrc[i] = (double)grad[o] * exp((double)src[i] - y[o]);
+        }
+      }
+    free(y);
+    return;
+  }
+  const int64_t cells = before * groups * after;
+  double* t = (double*)calloc((size_t)(cells > 0 ? cells : 1), sizeof(double));
+  for (int64_t b = 0; b < before; ++b)
+    for (int64_t l = 0; l < len; ++l) {
+      const int64_t g = index[l];
+      if (g < 0 || g >= groups) continue;
+      for (int64_t f = 0; f < after; ++f) {
+        const int64_t i = (b * len + l) * after + f;
+        t[(b * groups + g) * after + f] += mode == 0 ? y[i] * (double)grad[i] : (double)grad[i];
+      }
+    }
+  for (int64_t b = 0; b < before; ++b)
+    for (int64_t l = 0; l < len; ++l) {
+      const int64_t g = index[l];
+      if (g < 0 || g >= groups) continue;
+      for (int64_t f = 0; f < after; ++f) {
+        const int64_t i = (b * len + l) * after + f;
+        const double tt = t[(b * groups + g) * after + f];
+        gsrc[i] = mode == 0 ? y[i] * ((double)grad[i] - tt) : (double)grad[i] - exp(y[i]) * tt;
+      }
+    }
+  free(t);
+  free(y);
+}
+
 /* ---------------------------------------------------------------- SDDMM
  * reference test/sddmm_csr/arch22/golden.py:18-90: per edge e with row r
  * (ptr[r] <= e < ptr[r+1]) and column col[e], the operands are

@@ -54,6 +54,8 @@ def lib():
                                      ctypes.c_double, _f64p, vp]
         l.oracle_segment_lse.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, _f64p]
         l.oracle_group_softmax.argtypes = [_f32p, _i64p, i64, i64, i64, i64, ctypes.c_int, _f64p]
+        l.oracle_group_softmax_backward.argtypes = [_f32p, _f32p, _i64p, i64, i64, i64, i64, ctypes.c_int,
+                                                    _f64p]
         l.oracle_sddmm.argtypes = [_i64p, _i64p, i64, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, i64,
                                    _f64p]
         l.oracle_spmm_dgl.argtypes = [_i64p, _i64p, i64, vp, vp, i64, ctypes.c_int, ctypes.c_int, i64, _f64p]
@@ -226,6 +228,22 @@ def group_softmax(src, index, dim, groups, mode):
     shape = src.shape if m < 2 else src.shape[:dim] + (groups,) + src.shape[dim + 1:]
     out = np.zeros(shape, np.float64)
     lib().oracle_group_softmax(np.ascontiguousarray(src.reshape(-1)), idx, before, length, after, groups, m, out)
+    return out
+
+
+def group_softmax_backward(src, grad, index, dim, groups, mode):
+    """Gradient of group_softmax w.r.t. src from the float64 forward.  `grad`
+    has the forward output's shape (src-shaped, or `groups` along dim for
+    logsumexp).  Returns float64, src-shaped."""
+    src = _np(src, np.float32)
+    grad = _np(grad, np.float32)
+    idx = _np(index, np.int64).reshape(-1)
+    dim = dim % src.ndim
+    before, length, after = _split(src.shape, dim)
+    m = {"softmax": 0, "log_softmax": 1, "logsumexp": 2}[mode]
+    out = np.zeros(src.shape, np.float64)
+    lib().oracle_group_softmax_backward(np.ascontiguousarray(src.reshape(-1)), np.ascontiguousarray(grad.reshape(-1)),
+                                        idx, before, length, after, groups, m, out)
     return out
 
 

@@ -480,3 +480,52 @@ def test_spmm_dgl_messages_brute_force(op, width):
                 arr = np.stack(msgs)
                 ref = {"sum": arr.sum(0), "mean": arr.mean(0), "max": arr.max(0)}[reduce]
             np.testing.assert_allclose(got[r], ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+def test_group_softmax_backward_matches_torch_autograd(mode):
+    # autograd of torch's own float64 per-group softmax / log_softmax / logsumexp
+    rng = np.random.default_rng(15)
+    src = (rng.standard_normal((2, 25, 3)) * 4).astype(np.float32)
+    index = rng.integers(0, 6, size=25)
+    index[index == 2] = 3  # group 2 empty
+    gshape = (2, 6, 3) if mode == "logsumexp" else src.shape
+    grad = rng.standard_normal(gshape).astype(np.float32)
+    got = orc.group_softmax_backward(src, grad, index, 1, 6, mode)
+    t = torch.from_numpy(src).double().requires_grad_(True)
+    g = torch.from_numpy(grad).double()
+    outs = []
+    for grp in range(6):
+        pos = torch.from_numpy(np.nonzero(index == grp)[0])
+        if mode == "logsumexp":
+            if pos.numel():
+                outs.append((torch.logsumexp(t[:, pos], 1) * g[:, grp]).sum())
+        elif pos.numel():
+            fn = torch.softmax if mode == "softmax" else torch.log_softmax
+            outs.append((fn(t[:, pos], 1) * g[:, pos]).sum())
+    torch.stack(outs).sum().backward()
+    np.testing.assert_allclose(got, t.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+
+def test_group_softmax_backward_special_values_follow_torch():
+    # +inf / -inf groups give NaN gradients exactly where torch's autograd does
+    src = np.array([np.inf, 1.0, -np.inf, -np.inf, 0.5, 2.0], dtype=np.float32)
+    index = np.array([0, 0, 1, 1, 2, 2])
+    for mode in ("softmax", "log_softmax", "logsumexp"):
+        gshape = (3,) if mode == "logsumexp" else (6,)
+        grad = np.linspace(0.5, 1.5, gshape[0]).astype(np.float32)
+        got = orc.group_softmax_backward(src, grad, index, 0, 3, mode)
+        t = torch.from_numpy(src).double().requires_grad_(True)
+        g = torch.from_numpy(grad).double()
+        tot = 0
+        for grp in range(3):
+            sl = slice(2 * grp, 2 * grp + 2)
+            if mode == "logsumexp":
+                tot = tot + torch.logsumexp(t[sl], 0) * g[grp]
+            else:
+                fn = torch.softmax if mode == "softmax" else torch.log_softmax
+                tot = tot + (fn(t[sl], 0) * g[sl]).sum()
+        tot.backward()
+        ref = t.grad.numpy()
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref), err_msg=mode)
+        np.testing.assert_allclose(got[~np.isnan(ref)], ref[~np.isnan(ref)], rtol=1e-12, err_msg=mode)

@@ -166,6 +166,73 @@ def test_grouped_softmax_special_values(ogn, oracle, sorted_index):
         _softmax_check(ogn, oracle, src, index, 0, 4, mode, 1e-6)
 
 
+# Gradient tolerance: the reference's grouped-softmax tolerances
+# (test/common/grouped_softmax_golden.py:24-28), rtol = atol.
+GRAD_TOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 4e-2}
+
+
+def _softmax_grad_check(ogn, oracle, src, index, dim, groups, mode, tol, seed=0):
+    fn = {"softmax": ogn.scatter_softmax, "log_softmax": ogn.scatter_log_softmax,
+          "logsumexp": ogn.scatter_logsumexp}[mode]
+    x = src.cuda().requires_grad_(True)
+    out = fn(x, index.cuda(), dim, groups)
+    g = torch.from_numpy(np.random.default_rng(seed).standard_normal(tuple(out.shape)).astype(np.float32))
+    g = g.to(src.dtype)
+    out.backward(g.cuda())
+    assert x.grad.dtype == src.dtype and x.grad.shape == src.shape
+    gold = oracle.group_softmax_backward(src, g, index.long(), dim, groups, mode)
+    got = x.grad.float().cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(gold))
+    np.testing.assert_allclose(got, gold, rtol=tol, atol=tol, equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+@pytest.mark.parametrize("sorted_index", [True, False])
+def test_grouped_softmax_backward(ogn, oracle, dtype, mode, sorted_index):
+    rng = np.random.default_rng(53)
+    idx = rng.integers(0, 40, 2000)
+    idx[idx == 7] = 8  # an empty group
+    if sorted_index:
+        idx = np.sort(idx)
+    src = torch.from_numpy((rng.standard_normal((3, 2000, 4)) * 3).astype(np.float32)).to(dtype)
+    _softmax_grad_check(ogn, oracle, src, torch.from_numpy(idx), 1, 40, mode, GRAD_TOL[dtype])
+
+
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+def test_grouped_softmax_backward_edge_rows(ogn, oracle, mode):
+    # GAT layout: one score per edge grouped by destination row, hub rows of 4000
+    rng = np.random.default_rng(54)
+    deg = rng.poisson(40, size=300)
+    deg[::30] = 4000
+    idx = np.repeat(np.arange(300), deg)
+    src = torch.from_numpy((rng.standard_normal(idx.size) * 3).astype(np.float32))
+    _softmax_grad_check(ogn, oracle, src, torch.from_numpy(idx), 0, 300, mode, 1e-5, seed=1)
+
+
+@pytest.mark.parametrize("sorted_index", [True, False])
+def test_grouped_softmax_backward_special_values(ogn, oracle, sorted_index):
+    src = torch.tensor([INF, 1.0, -INF, -INF, 0.5, 2.0])
+    index = torch.tensor([0, 0, 1, 1, 2, 2])
+    if not sorted_index:
+        perm = torch.tensor([3, 5, 0, 2, 4, 1])
+        src, index = src[perm], index[perm]
+    for mode in ("softmax", "log_softmax", "logsumexp"):
+        _softmax_grad_check(ogn, oracle, src, index, 0, 3, mode, 1e-6)
+
+
+def test_grouped_softmax_backward_matches_torch_autograd(ogn):
+    # the same gradient as torch's own softmax autograd over one group per row
+    x = torch.randn(6, 50, dtype=torch.float32, device="cuda")
+    idx = torch.arange(6, device="cuda").repeat_interleave(50)
+    a = x.reshape(-1).clone().requires_grad_(True)
+    b = x.clone().requires_grad_(True)
+    g = torch.randn(300, device="cuda")
+    ogn.scatter_softmax(a, idx).backward(g)
+    torch.softmax(b, 1).reshape(-1).backward(g)
+    torch.testing.assert_close(a.grad, b.grad.reshape(-1), rtol=1e-5, atol=1e-6)
+
+
 def test_grouped_softmax_errors(ogn):
     src = torch.randn(6, device="cuda")
     with pytest.raises(ValueError, match="non-negative"):
