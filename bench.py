@@ -89,6 +89,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (rocprof counter calibration)")
+    ap.add_argument("--workload", choices=["spmm", "segment", "gat", "coo"], default="spmm",
+                    help="spmm = config 3 (the headline metric); segment / gat / coo = configs 2 / 4 / 5")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -96,6 +98,11 @@ def main():
               "hot path has no multi-GPU code here -- see DESIGN.md for how it would shard.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.workload != "spmm":
+        line = {"segment": bench_segment, "gat": bench_gat, "coo": bench_coo}[args.workload](args)
+        print(json.dumps(line), flush=True)
+        return
 
     import numpy as np
     import torch
@@ -206,6 +213,242 @@ def main():
     }
     print(json.dumps(result), flush=True)
 
+
+
+# ---------------------------------------------------------------- configs 2, 4, 5
+def _timed(fn, steps, warmup):
+    """Mean wall ms of fn() over `steps` calls after `warmup`, synchronised."""
+    import torch
+
+    for _ in range(max(warmup, 1)):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def _kernel_ms(fn, steps, names):
+    """Average per-call ms of the named library kernels (HIP events on the launch stream)."""
+    import torch
+    from ops_gnn import _lib
+
+    _lib.timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    res = {}
+    for n in names:
+        ms, cnt = _lib.timing_query(n)
+        res[n] = ms / steps if cnt else 0.0
+    _lib.timing_enable(False)
+    return res
+
+
+def _line(metric, value, unit, ms, args, dtype, workload, config, ops, roof_kernel, roof_bytes, roof_ms, cpu):
+    return {
+        "metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded PCG64, BASELINE recipe)",
+        "config": dict({"workload": workload}, **config), "ops": ops,
+        "roofline": {"bound": "hbm", "kernel": roof_kernel, "achieved": round(roof_bytes / roof_ms / 1e6, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(roof_bytes / roof_ms / 1e6 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": roof_bytes, "kernel_ms": round(roof_ms, 4)},
+        "cpu_baseline": cpu,
+    }
+
+
+def _cpu_sample(fn_rows, total_rows, bytes_of, budget_s=8.0):
+    """Time fn_rows(r) (the oracle on the first r rows/segments), growing r
+    until one run takes ~budget/4; returns (GB/s, rows, seconds)."""
+    rows = max(1, total_rows // 1000)
+    while True:
+        t0 = time.perf_counter()
+        fn_rows(rows)
+        dt = time.perf_counter() - t0
+        if dt >= budget_s / 4 or rows >= total_rows:
+            return bytes_of(rows) / dt / 1e9, rows, dt
+        rows = min(total_rows, int(rows * max(2.0, (budget_s / 4) / max(dt, 1e-3))))
+
+
+def bench_segment(args):
+    """Config 2: segment_csr sum/mean/max(+arg), segment_max_csr and
+    segment_logsumexp over src [1e6, 128] fp32 and 62 500 Poisson(16) segments."""
+    import numpy as np
+    import torch
+
+    import ops_gnn
+    from ops_gnn.synthetic import cfg2_segments
+
+    dev = torch.device("cuda:0")
+    src_np, ptr_np = cfg2_segments()
+    rows, k = src_np.shape
+    segs = ptr_np.shape[0] - 1
+    src = torch.from_numpy(src_np).to(dev)
+    ptr = torch.from_numpy(ptr_np).to(dev)
+    base = 4 * rows * k + 8 * (segs + 1) + 4 * segs * k
+    cases = [("sum", lambda: ops_gnn.segment_csr(src, ptr, reduce="sum"), base),
+             ("mean", lambda: ops_gnn.segment_csr(src, ptr, reduce="mean"), base),
+             ("max", lambda: ops_gnn.segment_max_csr(src, ptr), base + 8 * segs * k),
+             ("logsumexp", lambda: ops_gnn.segment_logsumexp(src, ptr), base)]
+    ops = {}
+    with torch.no_grad():
+        for name, fn, nbytes in cases:
+            ms = _timed(fn, args.steps, args.warmup)
+            kms = _kernel_ms(fn, args.steps, ["segment_main"])["segment_main"]
+            ops[name] = {"ms": round(ms, 4), "GB/s": round(nbytes / ms / 1e6, 1), "bytes": nbytes,
+                         "segment_main_ms": round(kms, 4)}
+            log(f"bench segment {name}: {ms:.4f} ms, {nbytes / ms / 1e6:.1f} GB/s (segment_main {kms:.4f} ms)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle
+
+        gbs, r, dt = _cpu_sample(
+            lambda r: oracle.segment_csr(src_np[: ptr_np[r]], ptr_np[: r + 1], "sum"), segs,
+            lambda r: 4 * int(ptr_np[r]) * k + 8 * (r + 1) + 4 * r * k)
+        cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": oracle.threads(), "kind": "port",
+               "sample": f"oracle_segment_csr sum (C, OpenMP, fp64 accumulate) on segments [0, {r}) "
+                         f"= {int(ptr_np[r])} rows of the same input, {dt:.2f} s"}
+    s = ops["sum"]
+    return _line("segment_csr sum effective HBM GB/s (config 2)", s["GB/s"], "GB/s", s["ms"], args, "f32",
+                 "configs[1]: segment reductions", {"rows": rows, "segments": segs, "k": k}, ops,
+                 "segment_main", base, s["segment_main_ms"], cpu)
+
+
+def bench_gat(args):
+    """Config 4: one GAT-style layer -- sddmm_csr(dot) of Q[row], K[col];
+    scatter_softmax over the edges of each row; SpMM-sum of the weights with V.
+    233 000 nodes, 114.6 M edges (lognormal degrees), fp16 features [., 64]."""
+    import numpy as np
+    import torch
+
+    import ops_gnn
+    from ops_gnn.synthetic import cfg4_gat_graph
+
+    dev = torch.device("cuda:0")
+
+    def gpu_sort(keys):
+        t = torch.from_numpy(keys).to(dev)
+        return torch.sort(t).values.cpu().numpy()
+
+    ptr_np, col_np, q_np, k_np, v_np = cfg4_gat_graph(sort_keys=gpu_sort)
+    n, f = q_np.shape
+    e = int(ptr_np[-1])
+    ptr = torch.from_numpy(ptr_np).to(dev)
+    col = torch.from_numpy(col_np).to(dev)
+    q = torch.from_numpy(q_np).to(dev).half()
+    kk = torch.from_numpy(k_np).to(dev).half()
+    v = torch.from_numpy(v_np).to(dev).half()
+    row = ops_gnn.ptr2ind(ptr, e)  # graph metadata: row of every edge (not timed)
+    log(f"bench gat: n={n} e={e} max_deg={int(np.diff(ptr_np).max())}")
+    state = {}
+
+    def sddmm():
+        state["s"] = ops_gnn.sddmm_csr(ptr, col, q, kk, "dot")
+
+    def softmax():
+        state["a"] = ops_gnn.scatter_softmax(state["s"], row, 0, n)
+
+    def spmm():
+        state["o"] = ops_gnn.csr_spmm(ptr, col, state["a"], v, "sum")
+
+    def layer():
+        sddmm()
+        softmax()
+        spmm()
+
+    eff = {"sddmm": 8 * e + 2 * e * f + 2 * e + 2 * n * f + 8 * (n + 1),
+           "softmax": 2 * e + 2 * e + 8 * e,
+           "spmm": 8 * e + 2 * e + 2 * e * f + 2 * n * f + 8 * (n + 1)}
+    comp = {"sddmm": 8 * e + 2 * e + 2 * 2 * n * f + 8 * (n + 1),
+            "softmax": eff["softmax"],
+            "spmm": 8 * e + 2 * e + 2 * 2 * n * f + 8 * (n + 1)}
+    ops = {}
+    with torch.no_grad():
+        layer()
+        for name, fn in (("sddmm", sddmm), ("softmax", softmax), ("spmm", spmm)):
+            ms = _timed(fn, args.steps, args.warmup)
+            ops[name] = {"ms": round(ms, 4), "effective_GB/s": round(eff[name] / ms / 1e6, 1),
+                         "compulsory_GB/s": round(comp[name] / ms / 1e6, 1)}
+            log(f"bench gat {name}: {ms:.4f} ms, effective {eff[name] / ms / 1e6:.1f} GB/s, "
+                f"compulsory {comp[name] / ms / 1e6:.1f} GB/s")
+        ms = _timed(layer, args.steps, args.warmup)
+        km = _kernel_ms(layer, args.steps, ["sddmm_main", "spmm_main", "group_apply", "segment_stats_main"])
+    tot_eff = sum(eff.values())
+    ops["layer"] = {"ms": round(ms, 4), "kernels_ms": {k2: round(v2, 4) for k2, v2 in km.items()}}
+    log(f"bench gat layer: {ms:.4f} ms; kernels {km}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle
+
+        qf, kf = q.float().cpu().numpy(), kk.float().cpu().numpy()
+
+        def cpu_rows(r):
+            oracle.sddmm(ptr_np[: r + 1], col_np[: ptr_np[r]], qf, kf, "dot")
+
+        gbs, r, dt = _cpu_sample(cpu_rows, n, lambda r: 8 * int(ptr_np[r]) + 2 * int(ptr_np[r]) * f)
+        cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": oracle.threads(), "kind": "port",
+               "sample": f"oracle_sddmm dot (C) on rows [0, {r}) = {int(ptr_np[r])} edges, {dt:.2f} s"}
+    return _line("GAT layer (sddmm + scatter_softmax + SpMM) effective GB/s (config 4)", tot_eff / ms / 1e6,
+                 "GB/s", ms, args, "f16", "configs[3]: GAT-style attention layer",
+                 {"nodes": n, "nnz": e, "k": f}, ops, "sddmm_main", eff["sddmm"], km["sddmm_main"], cpu)
+
+
+def bench_coo(args):
+    """Config 5: ind2ptr/ptr2ind round trip, scatter sum/mean/max,
+    scatter_log_softmax and scatter_logsumexp over a sorted destination index
+    (50 M edges, 1 M nodes, Zipf(1.8) in-degree), src [50 M, 32] fp32."""
+    import numpy as np
+    import torch
+
+    import ops_gnn
+    from ops_gnn.synthetic import cfg5_coo_scatter
+
+    dev = torch.device("cuda:0")
+    idx_np, src_np = cfg5_coo_scatter()
+    e, f = src_np.shape
+    nodes = 1_000_000
+    index = torch.from_numpy(idx_np).to(dev)
+    src = torch.from_numpy(src_np).to(dev)
+    ptr = ops_gnn.ind2ptr(index, nodes)
+    rt = ops_gnn.ptr2ind(ptr, e)
+    assert torch.equal(rt, index), "ind2ptr/ptr2ind round trip differs"
+    sb = 4 * e * f + 8 * e + 4 * nodes * f
+    cases = [("ind2ptr", lambda: ops_gnn.ind2ptr(index, nodes), 8 * e + 8 * (nodes + 1)),
+             ("ptr2ind", lambda: ops_gnn.ptr2ind(ptr, e), 8 * e + 8 * (nodes + 1)),
+             ("scatter_sum", lambda: ops_gnn.scatter(src, index, 0, dim_size=nodes, reduce="sum"), sb),
+             ("scatter_mean", lambda: ops_gnn.scatter(src, index, 0, dim_size=nodes, reduce="mean"), sb),
+             ("scatter_max", lambda: ops_gnn.scatter(src, index, 0, dim_size=nodes, reduce="max"),
+              sb + 8 * nodes * f),
+             ("scatter_log_softmax", lambda: ops_gnn.scatter_log_softmax(src, index, 0, nodes),
+              8 * e * f + 8 * e),
+             ("scatter_logsumexp", lambda: ops_gnn.scatter_logsumexp(src, index, 0, nodes), sb)]
+    ops = {}
+    with torch.no_grad():
+        for name, fn, nbytes in cases:
+            ms = _timed(fn, args.steps, args.warmup)
+            ops[name] = {"ms": round(ms, 4), "GB/s": round(nbytes / ms / 1e6, 1), "bytes": nbytes}
+            log(f"bench coo {name}: {ms:.4f} ms, {nbytes / ms / 1e6:.1f} GB/s")
+        kms = _kernel_ms(cases[2][1], args.steps, ["segment_main"])["segment_main"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle
+
+        ptr_np = ptr.cpu().numpy()
+
+        def cpu_rows(r):
+            oracle.scatter(src_np[: int(ptr_np[r])], idx_np[: ptr_np[r], None], 0, r, "sum")
+
+        gbs, r, dt = _cpu_sample(cpu_rows, nodes, lambda r: 4 * int(ptr_np[r]) * f + 8 * int(ptr_np[r]) + 4 * r * f)
+        cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": oracle.threads(), "kind": "port",
+               "sample": f"oracle_scatter sum (C) on nodes [0, {r}) = {int(ptr_np[r])} edges, {dt:.2f} s"}
+    s = ops["scatter_sum"]
+    return _line("scatter sum (sorted COO) effective HBM GB/s (config 5)", s["GB/s"], "GB/s", s["ms"], args, "f32",
+                 "configs[4]: COO scatter path", {"edges": e, "nodes": nodes, "k": f}, ops, "segment_main", sb,
+                 kms, cpu)
 
 if __name__ == "__main__":
     main()

@@ -38,8 +38,10 @@ namespace eng {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kUnroll = 8;
+constexpr int kUnrollSum = 8;
+constexpr int kUnrollWide = 4;
 constexpr int64_t kNone = INT64_MAX;
+constexpr int32_t kNone32 = INT32_MAX;
 
 // Reduction kinds (template parameter RK).
 enum { RK_SUM = 0, RK_MINMAX = 1, RK_LSE = 2 };
@@ -222,18 +224,35 @@ __global__ __launch_bounds__(256) void chunk_rows_kernel(Params p) {
   for (int64_t c = c0; c <= c1; ++c) cr[c] = r;
 }
 
-// FAST instances fix the common case at compile time -- messages x * w with
-// at most one weight per position, no product reduction, and the first-tie /
-// NaN-ignoring extremum rules -- which keeps the per-lane state small enough
-// for 6-7 waves per SIMD (the generic instance needs about twice the VGPRs).
-template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER, bool FAST>
-__global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
+// Variants.  V_FIRST and V_LATER fix the common cases at compile time --
+// messages x * w with at most one weight per position, no product
+// reduction, NaN-ignoring extrema with the first (V_FIRST) or the last
+// (V_LATER) tie winning -- which keeps the per-lane state small; V_GENERIC
+// reads every rule from Params.
+enum { V_GENERIC = 0, V_FIRST = 1, V_LATER = 2 };
+
+// Occupancy target per instance (waves per SIMD), enforced through the
+// register budget: 4 (<= 128 VGPRs) for the fast variants, 3 for 16-bit
+// min/max and log-sum-exp, whose 8 elements per lane need more state.
+template <int DT, int RK, int VAR>
+constexpr int engine_waves() {
+  return VAR == V_GENERIC ? 1 : (DT != OGN_F32 && RK != RK_SUM ? 3 : 4);
+}
+
+template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER, int VAR>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(engine_waves<DT, RK, VAR>())))
+void engine_kernel(Params p) {
   using E = Elem<DT>;
   using S_t = typename E::S;
+  constexpr bool FAST = VAR != V_GENERIC;
   constexpr int NE = VL ? E::VEC : 1;
   constexpr int S = kWave / G;
-  // min/max of fp32 compare exact fp64 products; fp16/bf16 products are exact in fp32.
-  using MT = std::conditional_t<RK == RK_MINMAX && DT == OGN_F32, double, float>;
+  // Steps in flight per wave: fewer for the wider min/max and log-sum-exp state.
+  constexpr int kUnroll = RK == RK_SUM ? kUnrollSum : kUnrollWide;
+  // min/max of weighted fp32 messages compare exact fp64 products (fp16/bf16
+  // products are exact in fp32); contiguous mode has no weights, so its fp32
+  // comparisons are exact as they are.
+  using MT = std::conditional_t<RK == RK_MINMAX && DT == OGN_F32 && GATHER, double, float>;
 
   const int lane = lane_id();
   const int sub = lane / G;
@@ -252,7 +271,7 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
   const S_t* __restrict__ val = static_cast<const S_t*>(p.val);
   const bool is_min = p.reduce == OGN_REDUCE_MIN;
   const bool is_prod = !FAST && p.reduce == OGN_REDUCE_PROD;
-  const bool later = !FAST && p.mm_mode == MM_LATER;
+  const bool later = VAR == V_LATER || (VAR == V_GENERIC && p.mm_mode == MM_LATER);
   const bool nanprop = !FAST && p.mm_mode == MM_NANPROP;
   const int vop = FAST ? (int)OP_MUL : p.val_op;
   const int val_mode = FAST ? std::min(p.val_mode, 1) : p.val_mode;
@@ -284,13 +303,15 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
 
   float acc[NE];
   MT best[NE];
-  int64_t barg[NE];
+  // Extremum positions are held as int32 offsets from the chunk start (a
+  // chunk is at most 8192 positions); kNone32 marks "nothing taken".
+  int32_t barg[NE];
   auto reset = [&]() {
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
       acc[i] = is_prod ? 1.f : 0.f;
       best[i] = RK == RK_LSE ? (MT)-__builtin_inff() : (MT)0;
-      barg[i] = kNone;
+      barg[i] = kNone32;
     }
   };
   reset();
@@ -306,16 +327,16 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
         if constexpr (RK == RK_MINMAX) {
           const MT ob = (MT)(sizeof(MT) == 8 ? shfld((double)best[i], lane ^ off)
                                              : shflf((float)best[i], lane ^ off));
-          const int64_t oa = shfl64(barg[i], lane ^ off);
+          const int32_t oa = shfl32(barg[i], lane ^ off);
           bool take;
           if (nanprop) {
-            take = oa != kNone && (barg[i] == kNone || (ob != ob) || better(ob, best[i], is_min));
+            take = oa != kNone32 && (barg[i] == kNone32 || (ob != ob) || better(ob, best[i], is_min));
           } else if (later) {
-            take = oa != kNone && (barg[i] == kNone || better(ob, best[i], is_min) ||
-                                   (ob == best[i] && oa > barg[i]));
+            take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
+                                     (ob == best[i] && oa > barg[i]));
           } else {
-            take = oa != kNone && (barg[i] == kNone || better(ob, best[i], is_min) ||
-                                   (ob == best[i] && oa < barg[i]));
+            take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
+                                     (ob == best[i] && oa < barg[i]));
           }
           if (take) {
             best[i] = ob;
@@ -347,7 +368,7 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
       if (!VL && k0 + i >= K) break;
       if constexpr (RK == RK_MINMAX) {
         static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)best[i];
-        (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i];
+        (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i] == kNone32 ? kNone : lo + barg[i];
       } else if constexpr (RK == RK_LSE) {
         static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2((float)best[i], acc[i]);
       } else {
@@ -365,7 +386,8 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
       int64_t ag[NE];
 #pragma unroll
       for (int i = 0; i < NE; ++i)
-        finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, acc[i], best[i], barg[i], &v[i], &ag[i]);
+        finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, acc[i], best[i],
+                            barg[i] == kNone32 ? kNone : lo + barg[i], &v[i], &ag[i]);
       const int64_t off = b * p.out_bstride + r * K + k0;
       if (VL || k0 + NE <= K) {
         store_floats<NE>(p.out, p.out_dt, off, v);
@@ -472,16 +494,16 @@ __global__ __launch_bounds__(kBlock) void engine_kernel(Params p) {
               if constexpr (RK == RK_MINMAX) {
                 const MT pv = apply_op<MT>((MT)x[i], (MT)wi, vop);
                 if (nanprop) {
-                  if (barg[i] == kNone || (pv != pv) || better(pv, best[i], is_min)) {
+                  if (barg[i] == kNone32 || (pv != pv) || better(pv, best[i], is_min)) {
                     best[i] = pv;
-                    barg[i] = e_mine;
+                    barg[i] = (int32_t)(e_mine - lo);
                   }
                 } else if (!(pv != pv)) {
-                  const bool take = barg[i] == kNone || better(pv, best[i], is_min) ||
+                  const bool take = barg[i] == kNone32 || better(pv, best[i], is_min) ||
                                     (later && pv == best[i]);
                   if (take) {
                     best[i] = pv;
-                    barg[i] = e_mine;
+                    barg[i] = (int32_t)(e_mine - lo);
                   }
                 }
               } else if constexpr (RK == RK_LSE) {
@@ -648,41 +670,51 @@ OGN_ENGINE_DECL(launch_contig_f16)
 OGN_ENGINE_DECL(launch_contig_bf16)
 #undef OGN_ENGINE_DECL
 
-template <int DT, typename IDX, bool VL, int RK, bool GATHER, bool FAST>
+template <int DT, typename IDX, bool VL, int RK, bool GATHER, int VAR>
 void launch_g(int g, dim3 grid, hipStream_t s, const Params& p) {
   switch (g) {
 #define OGN_G(GV) \
-  case GV: hipLaunchKernelGGL((engine_kernel<DT, IDX, GV, VL, RK, GATHER, FAST>), grid, dim3(kBlock), 0, s, p); break;
+  case GV: hipLaunchKernelGGL((engine_kernel<DT, IDX, GV, VL, RK, GATHER, VAR>), grid, dim3(kBlock), 0, s, p); break;
     OGN_G(1) OGN_G(2) OGN_G(4) OGN_G(8) OGN_G(16) OGN_G(32) OGN_G(64)
 #undef OGN_G
     default: break;
   }
 }
 
-template <int DT, typename IDX, int RK, bool GATHER, bool FAST>
+template <int DT, typename IDX, int RK, bool GATHER, int VAR>
 void launch_rk_f(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
   if (pl.vec) {
-    launch_g<DT, IDX, true, RK, GATHER, FAST>(pl.g, grid, s, p);
+    launch_g<DT, IDX, true, RK, GATHER, VAR>(pl.g, grid, s, p);
   } else if (pl.g == 1) {
-    hipLaunchKernelGGL((engine_kernel<DT, IDX, 1, false, RK, GATHER, FAST>), grid, dim3(kBlock), 0, s, p);
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 1, false, RK, GATHER, VAR>), grid, dim3(kBlock), 0, s, p);
   } else {
-    hipLaunchKernelGGL((engine_kernel<DT, IDX, 64, false, RK, GATHER, FAST>), grid, dim3(kBlock), 0, s, p);
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 64, false, RK, GATHER, VAR>), grid, dim3(kBlock), 0, s, p);
   }
 }
 
-// The FAST instance covers requests whose messages are x * w with a scalar
-// (or no) weight, that do not multiply, and whose extremum rule is first-tie
-// with NaN ignored (torch_sparse SpMM, segment_csr).
-inline bool fast_ok(int rk, const Params& p) {
-  if (p.val_op != OP_MUL || p.val_mode == 2 || p.reduce == OGN_REDUCE_PROD) return false;
-  if (rk == RK_MINMAX) return p.mm_mode == MM_SPMM || p.mm_mode == MM_SEGCSR;
-  return true;
+// Which variant serves a request: the fast ones need x * w messages with a
+// scalar (or no) weight, no product reduction, and for min/max the
+// NaN-ignoring first-tie rule (torch_sparse SpMM, segment_csr) or, in
+// contiguous mode, the later-tie rule (segment_coo, sorted scatter).
+inline int variant_of(int rk, bool gather, const Params& p) {
+  if (p.val_op != OP_MUL || p.val_mode == 2 || p.reduce == OGN_REDUCE_PROD) return V_GENERIC;
+  if (rk != RK_MINMAX) return V_FIRST;
+  if (p.mm_mode == MM_SPMM || p.mm_mode == MM_SEGCSR) return V_FIRST;
+  if (!gather && p.mm_mode == MM_LATER) return V_LATER;
+  return V_GENERIC;
 }
 
 template <int DT, typename IDX, int RK, bool GATHER>
 void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
-  if (fast_ok(RK, p)) launch_rk_f<DT, IDX, RK, GATHER, true>(pl, grid, s, p);
-  else launch_rk_f<DT, IDX, RK, GATHER, false>(pl, grid, s, p);
+  const int v = variant_of(RK, GATHER, p);
+  if constexpr (!GATHER && RK == RK_MINMAX) {
+    if (v == V_LATER) {
+      launch_rk_f<DT, IDX, RK, GATHER, V_LATER>(pl, grid, s, p);
+      return;
+    }
+  }
+  if (v == V_FIRST) launch_rk_f<DT, IDX, RK, GATHER, V_FIRST>(pl, grid, s, p);
+  else launch_rk_f<DT, IDX, RK, GATHER, V_GENERIC>(pl, grid, s, p);
 }
 
 // Gather mode (SpMM) instantiates int32 and int64 indices with sum / min-max;

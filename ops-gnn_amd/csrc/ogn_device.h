@@ -33,6 +33,47 @@ class TimedLaunch {
   bool active_ = false;
 };
 
+// ---------------------------------------------------------------- invariant division
+// n / d for 0 <= n < 2^63 and a divisor d >= 1 fixed at launch:
+// q = (umulhi(n, m) + n) >> l with l = ceil(log2 d) and
+// m = floor(2^64 (2^l - d) / d) + 1 (T. Granlund, P. Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994, section 4).  Replaces
+// the software 64-bit division in per-element index arithmetic.
+struct FastDiv {
+  uint64_t d;
+  uint64_t m;
+  int l;
+};
+
+inline FastDiv make_fastdiv(int64_t d) {
+  FastDiv f{};
+  f.d = (uint64_t)(d < 1 ? 1 : d);
+  f.l = 0;
+  while ((1ull << f.l) < f.d) ++f.l;
+  const unsigned __int128 one = 1;
+  f.m = (uint64_t)(((one << 64) * ((one << f.l) - f.d)) / f.d + 1);
+  return f;
+}
+
+__device__ __forceinline__ int64_t fdiv(int64_t n, const FastDiv& f) {
+  const uint64_t hi = __umul64hi((uint64_t)n, f.m);
+  return (int64_t)((hi + (uint64_t)n) >> f.l);
+}
+
+// i = (b * len + l) * after + k  ->  (b, l, k) for a [before, len, after] tensor.
+struct Split3 {
+  FastDiv after, len;
+};
+
+inline Split3 make_split3(int64_t len, int64_t after) { return Split3{make_fastdiv(after), make_fastdiv(len)}; }
+
+__device__ __forceinline__ void split3(int64_t i, const Split3& s, int64_t& b, int64_t& l, int64_t& k) {
+  const int64_t t = fdiv(i, s.after);
+  k = i - t * (int64_t)s.after.d;
+  b = fdiv(t, s.len);
+  l = t - b * (int64_t)s.len.d;
+}
+
 // ---------------------------------------------------------------- codecs
 // bf16 <-> fp32: a bf16 is the high half of an fp32; narrowing rounds to
 // nearest-even on the 16 discarded bits and keeps NaNs quiet.

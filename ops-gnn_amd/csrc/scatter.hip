@@ -46,6 +46,7 @@ struct ScatterArgs {
   int reduce;
   int has_out;
   float limit;
+  Split3 sp;  // index split of [before, len, after]
 };
 
 __global__ __launch_bounds__(256) void scatter_init_kernel(ScatterArgs a) {
@@ -78,9 +79,8 @@ __global__ __launch_bounds__(256) void scatter_main_kernel(ScatterArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t f = i % a.after;
-    const int64_t l = (i / a.after) % a.len;
-    const int64_t b = i / (a.after * a.len);
+    int64_t b, l, f;
+    split3(i, a.sp, b, l, f);
     const int64_t t = a.index[b * a.isb + l * a.isl + f * a.isf];
     if (t < 0 || t >= a.size) continue;
     const float x = load_float(a.src, a.dt, i);
@@ -108,9 +108,8 @@ __global__ __launch_bounds__(256) void scatter_arg_kernel(ScatterArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t f = i % a.after;
-    const int64_t l = (i / a.after) % a.len;
-    const int64_t b = i / (a.after * a.len);
+    int64_t b, l, f;
+    split3(i, a.sp, b, l, f);
     const int64_t t = a.index[b * a.isb + l * a.isl + f * a.isf];
     if (t < 0 || t >= a.size) continue;
     const float x = load_float(a.src, a.dt, i);
@@ -162,6 +161,7 @@ struct GroupArgs {
   uint32_t* key;
   void* out;
   int mode;  // 0 softmax, 1 log_softmax
+  Split3 sp;
 };
 
 __device__ __forceinline__ int64_t group_of(const GroupArgs& a, int64_t l) {
@@ -181,9 +181,8 @@ __global__ __launch_bounds__(256) void group_max_kernel(GroupArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t f = i % a.after;
-    const int64_t l = (i / a.after) % a.len;
-    const int64_t b = i / (a.after * a.len);
+    int64_t b, l, f;
+    split3(i, a.sp, b, l, f);
     const int64_t g = group_of(a, l);
     if (g < 0 || g >= a.groups) continue;
     const float x = load_float(a.src, a.dt, i);
@@ -195,9 +194,8 @@ __global__ __launch_bounds__(256) void group_sum_kernel(GroupArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t f = i % a.after;
-    const int64_t l = (i / a.after) % a.len;
-    const int64_t b = i / (a.after * a.len);
+    int64_t b, l, f;
+    split3(i, a.sp, b, l, f);
     const int64_t g = group_of(a, l);
     if (g < 0 || g >= a.groups) continue;
     const int64_t o = (b * a.groups + g) * a.after + f;
@@ -219,9 +217,8 @@ __global__ __launch_bounds__(256) void group_apply_kernel(GroupArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t f = i % a.after;
-    const int64_t l = (i / a.after) % a.len;
-    const int64_t b = i / (a.after * a.len);
+    int64_t b, l, f;
+    split3(i, a.sp, b, l, f);
     const int64_t g = group_of(a, l);
     float v = 0.f;
     if (g >= 0 && g < a.groups) {
@@ -261,6 +258,7 @@ struct GroupBwdArgs {
   float* total;  // [b, groups, f] fp32 group sums (zeroed by the caller of the sum pass)
   void* grad_src;
   int mode;  // 0 softmax, 1 log_softmax, 2 logsumexp
+  Split3 sp;
 };
 
 __device__ __forceinline__ int64_t bwd_group_of(const GroupBwdArgs& a, int64_t l) {
@@ -287,9 +285,8 @@ __global__ __launch_bounds__(256) void group_bwd_sum_kernel(GroupBwdArgs a) {
     int64_t key = -1;
     float v = 0.f;
     if (i < total) {
-      const int64_t f = i % a.after;
-      const int64_t l = (i / a.after) % a.len;
-      const int64_t b = i / (a.after * a.len);
+      int64_t b, l, f;
+      split3(i, a.sp, b, l, f);
       const int64_t g = bwd_group_of(a, l);
       if (g >= 0 && g < a.groups) {
         key = (b * a.groups + g) * a.after + f;
@@ -321,9 +318,8 @@ __global__ __launch_bounds__(256) void group_bwd_apply_kernel(GroupBwdArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t f = i % a.after;
-    const int64_t l = (i / a.after) % a.len;
-    const int64_t b = i / (a.after * a.len);
+    int64_t b, l, f;
+    split3(i, a.sp, b, l, f);
     const int64_t g = bwd_group_of(a, l);
     float v = 0.f;
     if (g >= 0 && g < a.groups) {
@@ -386,6 +382,7 @@ int ogn_scatter_atomic(const void* src, int dtype, const int64_t* index, int64_t
   a.before = before;
   a.len = len;
   a.after = after;
+  a.sp = make_split3(len, after);
   a.size = size;
   a.out = out;
   a.arg = (reduce == OGN_REDUCE_MIN || reduce == OGN_REDUCE_MAX) ? arg : nullptr;
@@ -438,6 +435,7 @@ int ogn_group_stats_atomic(const void* src, int dtype, const void* index, int in
   a.before = before;
   a.len = len;
   a.after = after;
+  a.sp = make_split3(len, after);
   a.groups = groups;
   a.m = m;
   a.s = s_out;
@@ -473,6 +471,7 @@ int ogn_group_softmax_apply(const void* src, int dtype, const void* index, int i
   a.before = before;
   a.len = len;
   a.after = after;
+  a.sp = make_split3(len, after);
   a.groups = groups;
   a.m = const_cast<float*>(m);
   a.s = const_cast<float*>(s);
@@ -532,6 +531,7 @@ int ogn_group_softmax_backward(const void* saved, const void* grad, const void* 
   a.before = before;
   a.len = len;
   a.after = after;
+  a.sp = make_split3(len, after);
   a.groups = groups;
   a.total = workspace;
   a.grad_src = grad_src;

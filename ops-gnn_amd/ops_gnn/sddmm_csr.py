@@ -10,7 +10,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from . import _lib
+from . import _lib, _native
 from ._lib import check, dptr, lib, stream_of
 
 _MESSAGE_OPS = {"dot", "add", "sub", "mul", "div", "copy_lhs", "copy_rhs"}
@@ -57,6 +57,31 @@ def _check_operand(name: str, value, required: bool) -> None:
         raise ValueError(f"sddmm_csr: {name} must be float16, bfloat16 or float32")
 
 
+# Validation results per (indices version, indptr version, dst rows): the
+# reference re-validates on every call (sddmm_csr.cpp:78-126); a mutated
+# tensor bumps its version and is checked again.
+_CSR_CHECKS = _native._VersionCache(limit=128)
+
+
+def _csr_status(indptr, indices, m, nnz, n) -> int:
+    import weakref
+
+    per_indices = _CSR_CHECKS.get(indices, dict)
+    key = (id(indptr), indptr.data_ptr(), indptr._version, n)
+    hit = per_indices.get(key)
+    if hit is not None and hit[0]() is indptr:
+        return hit[1]
+    status = torch.empty(1, dtype=torch.int32, device=indptr.device)
+    check(lib.ogn_validate_csr(dptr(indptr.contiguous()), dptr(indices.contiguous()),
+                               _lib.I64 if indptr.dtype == torch.int64 else _lib.I32, m, nnz, n, dptr(status),
+                               stream_of(indptr)), "sddmm_csr")
+    code = int(status.item())
+    if len(per_indices) > 8:
+        per_indices.clear()
+    per_indices[key] = (weakref.ref(indptr), code)
+    return code
+
+
 def _check_csr(indptr, indices, lhs, rhs, lt, rt, use_l, use_r):
     """reference csrc/npu/sddmm_csr/op_host/sddmm_csr.cpp:78-126 (CheckCsr) and
     CheckTargetRange: one fused device check, one small host read."""
@@ -71,11 +96,7 @@ def _check_csr(indptr, indices, lhs, rhs, lt, rt, use_l, use_r):
     if use_r and rt == 2:
         dst_rows.append(rhs.size(0))
     n = min(dst_rows) if dst_rows else (1 << 62)
-    status = torch.empty(1, dtype=torch.int32, device=indptr.device)
-    check(lib.ogn_validate_csr(dptr(indptr.contiguous()), dptr(indices.contiguous()),
-                               _lib.I64 if indptr.dtype == torch.int64 else _lib.I32, m, nnz, n, dptr(status),
-                               stream_of(indptr)), "sddmm_csr")
-    code = int(status.item())
+    code = _csr_status(indptr, indices, m, nnz, n)
     if code == 2:
         raise RuntimeError("sddmm_csr: CSR indices are out of range for dst features")
     if code:
