@@ -121,8 +121,8 @@ __device__ __forceinline__ float clampf_max(float m) {
 __device__ __forceinline__ void lse_merge(float& m, float& s, float om, float os) {
   const float nm = fmaxf(m, om);
   const float cn = clampf_max(nm);
-  const float a = s == 0.f ? 0.f : s * expf(clampf_max(m) - cn);
-  const float bb = os == 0.f ? 0.f : os * expf(clampf_max(om) - cn);
+  const float a = s == 0.f ? 0.f : s * fast_exp(clampf_max(m) - cn);
+  const float bb = os == 0.f ? 0.f : os * fast_exp(clampf_max(om) - cn);
   m = nm;
   s = a + bb;
 }
@@ -130,10 +130,10 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, float om, float os
 __device__ __forceinline__ void lse_add(float& m, float& s, float x) {
   if (x > m) {
     const float cn = clampf_max(x);
-    s = (s == 0.f ? 0.f : s * expf(clampf_max(m) - cn)) + expf(x - cn);
+    s = (s == 0.f ? 0.f : s * fast_exp(clampf_max(m) - cn)) + fast_exp(x - cn);
     m = x;
   } else {
-    s += expf(x - clampf_max(m));
+    s += fast_exp(x - clampf_max(m));
   }
 }
 

@@ -33,6 +33,17 @@ class TimedLaunch {
   bool active_ = false;
 };
 
+// ---------------------------------------------------------------- exponential
+// e^x through the hardware base-2 exponential (v_exp_f32): exp2(x * log2 e).
+// The rounded product adds a relative error of about |x| * 2^-24 to the
+// ~1 ulp of exp2, so terms far below the largest one (|x| large) carry a
+// larger relative but negligible absolute error -- the regime of log-sum-exp
+// and softmax, where every term is exp(x - max) <= 1.  exp2(+-inf) and NaN
+// behave as IEEE.
+__device__ __forceinline__ float fast_exp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
 // ---------------------------------------------------------------- invariant division
 // n / d for 0 <= n < 2^63 and a divisor d >= 1 fixed at launch:
 // q = (umulhi(n, m) + n) >> l with l = ceil(log2 d) and

@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void group_sum_kernel(GroupArgs a) {
     if (g < 0 || g >= a.groups) continue;
     const int64_t o = (b * a.groups + g) * a.after + f;
     const float x = load_float(a.src, a.dt, i);
-    atomicAdd(&a.s[o], expf(x - clampm(float_of(a.key[o]))));
+    atomicAdd(&a.s[o], fast_exp(x - clampm(float_of(a.key[o]))));
   }
 }
 
@@ -213,6 +213,13 @@ __global__ __launch_bounds__(256) void group_keys_to_max_kernel(GroupArgs a) {
 
 // softmax: exp(x - clamp(m)) / s;  log_softmax: (x - clamp(m)) - log(s).
 // A group holding +inf (m = +inf) is NaN throughout, as torch.softmax gives.
+__device__ __forceinline__ float group_apply_one(const GroupArgs& a, float x, float m, float s) {
+  const float d = x - clampm(m);
+  float v = a.mode == 0 ? fast_exp(d) / s : d - logf(s);
+  if (m == __builtin_inff()) v = __builtin_nanf("");
+  return v;
+}
+
 __global__ __launch_bounds__(256) void group_apply_kernel(GroupArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -223,13 +230,47 @@ __global__ __launch_bounds__(256) void group_apply_kernel(GroupArgs a) {
     float v = 0.f;
     if (g >= 0 && g < a.groups) {
       const int64_t o = (b * a.groups + g) * a.after + f;
-      const float m = a.m[o], s = a.s[o];
-      const float x = load_float(a.src, a.dt, i);
-      const float d = x - clampm(m);
-      v = a.mode == 0 ? expf(d) / s : d - logf(s);
-      if (m == __builtin_inff()) v = __builtin_nanf("");
+      v = group_apply_one(a, load_float(a.src, a.dt, i), a.m[o], a.s[o]);
     }
     store_floats<1>(a.out, a.dt, i, &v);
+  }
+}
+
+// The same, one 16-byte packet of src / out per thread (4 fp32 or 8 fp16 /
+// bf16 features of one position) when after is a multiple of the packet:
+// the index and the (b, l) split are read once per packet and m / s come in
+// 16-byte loads.
+template <int DT>
+__global__ __launch_bounds__(256) void group_apply_vec_kernel(GroupArgs a) {
+  using E = Elem<DT>;
+  constexpr int NE = E::VEC;
+  const int64_t packets = a.before * a.len * a.after / NE;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const typename E::S* __restrict__ src = static_cast<const typename E::S*>(a.src);
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < packets; p += stride) {
+    const int64_t i0 = p * NE;
+    int64_t b, l, f;
+    split3(i0, a.sp, b, l, f);
+    const int64_t g = group_of(a, l);
+    float v[NE];
+    if (g >= 0 && g < a.groups) {
+      float x[NE];
+      E::unpack(load16(src + i0), x);
+      const int64_t o = (b * a.groups + g) * a.after + f;
+#pragma unroll
+      for (int j = 0; j < NE; j += 4) {
+        const float4 m4 = *reinterpret_cast<const float4*>(a.m + o + j);
+        const float4 s4 = *reinterpret_cast<const float4*>(a.s + o + j);
+        v[j] = group_apply_one(a, x[j], m4.x, s4.x);
+        v[j + 1] = group_apply_one(a, x[j + 1], m4.y, s4.y);
+        v[j + 2] = group_apply_one(a, x[j + 2], m4.z, s4.z);
+        v[j + 3] = group_apply_one(a, x[j + 3], m4.w, s4.w);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NE; ++j) v[j] = 0.f;
+    }
+    store_floats<NE>(a.out, DT, i0, v);
   }
 }
 
@@ -478,7 +519,17 @@ int ogn_group_softmax_apply(const void* src, int dtype, const void* index, int i
   a.out = out;
   a.mode = log_softmax ? 1 : 0;
   TimedLaunch t("group_apply", st);
-  hipLaunchKernelGGL(group_apply_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);
+  const int ne = 16 / dtype_size(dtype);
+  const bool vec = after % ne == 0 && (uintptr_t)src % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                   (uintptr_t)m % 16 == 0 && (uintptr_t)s % 16 == 0;
+  if (vec) {
+    const dim3 g(grid_for(total / ne));
+    if (dtype == OGN_F32) hipLaunchKernelGGL(group_apply_vec_kernel<OGN_F32>, g, dim3(256), 0, st, a);
+    else if (dtype == OGN_F16) hipLaunchKernelGGL(group_apply_vec_kernel<OGN_F16>, g, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(group_apply_vec_kernel<OGN_BF16>, g, dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(group_apply_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);
+  }
   return check_launch("ogn_group_softmax_apply");
 }
 

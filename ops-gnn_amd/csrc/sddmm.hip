@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void sddmm_chunk_rows(const IDX* __restrict__ 
 }
 
 template <int DT, typename IDX, int G, bool VL>
-__global__ __launch_bounds__(kBlock) void sddmm_kernel(SddmmParams p) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void sddmm_kernel(SddmmParams p) {
   using E = Elem<DT>;
   using S_t = typename E::S;
   constexpr int NE = VL ? E::VEC : 1;
@@ -86,16 +86,23 @@ __global__ __launch_bounds__(kBlock) void sddmm_kernel(SddmmParams p) {
   };
   int64_t re = need_row ? rowend(r) : kNoRow;
 
+  // An operand gathered by row (target 0) is loaded once per row change of
+  // the sub-group and kept in registers; `held_*` is the row it holds.
+  int64_t held_l = -1, held_r = -1;
+  uint4 keep_l = make_uint4(0u, 0u, 0u, 0u), keep_r = keep_l;
+
   for (int64_t wbase = lo; wbase < hi; wbase += kWave) {
     const int64_t el = wbase + lane;
     int64_t cl = el < hi ? (int64_t)load_stream(col + el) : 0;
     const int nw = (int)std::min<int64_t>(kWave, hi - wbase);
     const int nsteps = (nw + S - 1) / S;
     for (int j0 = 0; j0 < nsteps; j0 += kU) {
-      int64_t row[kU];
+      // Phase 1: rows of the U steps (wave-uniform walk) and column shuffles.
+      int64_t row[kU], cc[kU];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         row[u] = 0;
+        cc[u] = (int64_t)shfl64(cl, ((j0 + u) * S + sub) & (kWave - 1));
         if (!need_row || j0 + u >= nsteps) continue;
         const int64_t e_first = wbase + (int64_t)(j0 + u) * S;
         const int64_t last = std::min<int64_t>(e_first + S, hi) - 1;
@@ -111,54 +118,69 @@ __global__ __launch_bounds__(kBlock) void sddmm_kernel(SddmmParams p) {
           re = rowend(r);
         }
       }
-      float xl[kU][NE], xr[kU][NE];
-      int64_t eidx[kU];
-      bool ok[kU];
       float dsum[kU];
 #pragma unroll
       for (int u = 0; u < kU; ++u) dsum[u] = 0.f;
       for (int64_t kp = 0; kp < kpass; ++kp) {
         const int64_t k0 = VL ? (int64_t)gl * NE : kp * G + gl;
         const bool kok = VL || k0 < K;
+        // Phase 2: issue every gather of the U steps back to back (raw).
+        uint4 rl[kU], rr[kU];
+        float sl[kU], sr[kU];
+        bool ok[kU], new_l[kU], new_r[kU];
+        int64_t pl_ = held_l, pr_ = held_r;
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
           const int idx = (j0 + u) * S + sub;
-          const int64_t cc = (int64_t)shfl64(cl, idx & (kWave - 1));
           const int64_t e = wbase + idx;
-          eidx[u] = e;
           ok[u] = (j0 + u) < nsteps && idx < nw;
-          const int64_t li = p.lt == 0 ? row[u] : (p.lt == 1 ? e : cc);
-          const int64_t ri = p.rt == 0 ? row[u] : (p.rt == 1 ? e : cc);
+          const int64_t li = p.lt == 0 ? row[u] : (p.lt == 1 ? e : cc[u]);
+          const int64_t ri = p.rt == 0 ? row[u] : (p.rt == 1 ? e : cc[u]);
           const bool lok = ok[u] && kok && use_l && li >= 0 && li < p.lhs_rows;
           const bool rok = ok[u] && kok && use_r && ri >= 0 && ri < p.rhs_rows;
+          // reuse only in vector mode (one pass holds the whole feature row)
+          new_l[u] = !(VL && p.lt == 0 && li == pl_);
+          new_r[u] = !(VL && p.rt == 0 && ri == pr_);
+          if (VL && p.lt == 0 && ok[u]) pl_ = li;
+          if (VL && p.rt == 0 && ok[u]) pr_ = ri;
+          rl[u] = make_uint4(0u, 0u, 0u, 0u);
+          rr[u] = rl[u];
+          sl[u] = 0.f;
+          sr[u] = 0.f;
           if constexpr (VL) {
-            if (lok) {
-              E::unpack(load16(lhs + li * K + k0), xl[u]);
-            } else {
-#pragma unroll
-              for (int i = 0; i < NE; ++i) xl[u][i] = 0.f;
-            }
-            if (rok) {
-              E::unpack(load16(rhs + ri * K + k0), xr[u]);
-            } else {
-#pragma unroll
-              for (int i = 0; i < NE; ++i) xr[u][i] = 0.f;
-            }
+            if (lok && new_l[u]) rl[u] = load16(lhs + li * K + k0);
+            if (rok && new_r[u]) rr[u] = load16(rhs + ri * K + k0);
           } else {
-            xl[u][0] = lok ? E::load1(lhs, li * K + k0) : 0.f;
-            xr[u][0] = rok ? E::load1(rhs, ri * K + k0) : 0.f;
+            if (lok) sl[u] = E::load1(lhs, li * K + k0);
+            if (rok) sr[u] = E::load1(rhs, ri * K + k0);
           }
+          if (!lok) new_l[u] = true;  // a skipped operand reads as zero
+          if (!rok) new_r[u] = true;
         }
+        held_l = pl_;
+        held_r = pr_;
+        // Phase 3: consume in order.
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
+          float xl[NE], xr[NE];
+          if constexpr (VL) {
+            // steps past the end of the window leave the held rows alone
+            if (ok[u] && new_l[u]) keep_l = rl[u];
+            if (ok[u] && new_r[u]) keep_r = rr[u];
+            E::unpack(keep_l, xl);
+            E::unpack(keep_r, xr);
+          } else {
+            xl[0] = sl[u];
+            xr[0] = sr[u];
+          }
           if (p.op == SD_DOT) {
 #pragma unroll
-            for (int i = 0; i < NE; ++i) dsum[u] = __builtin_fmaf(xl[u][i], xr[u][i], dsum[u]);
+            for (int i = 0; i < NE; ++i) dsum[u] = __builtin_fmaf(xl[i], xr[i], dsum[u]);
           } else if (ok[u] && kok) {
             float v[NE];
 #pragma unroll
             for (int i = 0; i < NE; ++i) {
-              const float a = xl[u][i], b = xr[u][i];
+              const float a = xl[i], b = xr[i];
               switch (p.op) {
                 case SD_ADD: v[i] = a + b; break;
                 case SD_SUB: v[i] = a - b; break;
@@ -168,7 +190,7 @@ __global__ __launch_bounds__(kBlock) void sddmm_kernel(SddmmParams p) {
                 default: v[i] = b; break;
               }
             }
-            store_floats<NE>(p.out, p.dt, eidx[u] * K + k0, v);
+            store_floats<NE>(p.out, p.dt, (wbase + (j0 + u) * S + sub) * K + k0, v);
           }
         }
       }
@@ -182,7 +204,8 @@ __global__ __launch_bounds__(kBlock) void sddmm_kernel(SddmmParams p) {
             const float o = shflf(d, lane ^ off);
             d = (lane & off) ? o + d : d + o;
           }
-          if (gl == 0 && ok[u]) store_floats<1>(p.out, p.dt, eidx[u], &d);
+          const int idx = (j0 + u) * S + sub;
+          if (gl == 0 && (j0 + u) < nsteps && idx < nw) store_floats<1>(p.out, p.dt, wbase + idx, &d);
         }
       }
     }
