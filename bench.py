@@ -49,6 +49,19 @@ def read_traffic(dtype):
     return None
 
 
+def copy_calibration():
+    """Three 1 GiB device-to-device copies: known bytes for scaling rocprof's
+    FETCH_SIZE / WRITE_SIZE counters in the same process."""
+    import torch
+
+    src = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def cpu_baseline(ptr, col, val, mat, k, budget_s=12.0):
     """Time the oracle (C + OpenMP) on a prefix of rows, growing the sample
     until one run takes >= ~1/4 of the budget; report GB/s of that sample."""
@@ -101,6 +114,8 @@ def main():
 
     if args.workload != "spmm":
         line = {"segment": bench_segment, "gat": bench_gat, "coo": bench_coo}[args.workload](args)
+        if args.copy_calibration:
+            copy_calibration()
         print(json.dumps(line), flush=True)
         return
 
@@ -157,12 +172,7 @@ def main():
         _lib.timing_enable(False)
 
         if args.copy_calibration:
-            src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
-            dst = torch.empty_like(src)
-            for _ in range(3):
-                dst.copy_(src)
-            torch.cuda.synchronize()
-            del src, dst
+            copy_calibration()
 
     esz = 4 if args.dtype == "f32" else 2
     mm = args.reduce in ("min", "max")

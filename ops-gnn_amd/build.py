@@ -38,6 +38,9 @@ COMMON_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # let `#pragma unroll` fully unroll the engine's consume loop (its body
+    # holds the row-finishing code) so that staged loads stay in registers
+    "-mllvm", "-pragma-unroll-threshold=200000",
 ]
 
 

@@ -229,7 +229,10 @@ __global__ __launch_bounds__(256) void chunk_rows_kernel(Params p) {
 // reduction, NaN-ignoring extrema with the first (V_FIRST) or the last
 // (V_LATER) tie winning -- which keeps the per-lane state small; V_GENERIC
 // reads every rule from Params.
-enum { V_GENERIC = 0, V_FIRST = 1, V_LATER = 2 };
+// V_FIRST32 is V_FIRST for a gathered operand below 4 GiB: row offsets are
+// 32-bit byte offsets from a uniform base (one VGPR per address, one
+// ds_bpermute per column).
+enum { V_GENERIC = 0, V_FIRST = 1, V_LATER = 2, V_FIRST32 = 3 };
 
 // Occupancy target per instance (waves per SIMD), enforced through the
 // register budget: 4 (<= 128 VGPRs) for the fast variants, 3 for 16-bit
@@ -245,6 +248,8 @@ void engine_kernel(Params p) {
   using E = Elem<DT>;
   using S_t = typename E::S;
   constexpr bool FAST = VAR != V_GENERIC;
+  constexpr bool OFF32 = VAR == V_FIRST32;
+  static_assert(!OFF32 || (VL && GATHER), "32-bit offsets are for vector gathers");
   constexpr int NE = VL ? E::VEC : 1;
   constexpr int S = kWave / G;
   // Steps in flight per wave: fewer for the wider min/max and log-sum-exp state.
@@ -316,48 +321,55 @@ void engine_kernel(Params p) {
   };
   reset();
 
+  // One butterfly round over sub-groups OFF apart (OFF a compile-time lane
+  // distance, see xor_shfl).
+  auto combine_round = [&](auto offc) {
+    constexpr int off = decltype(offc)::value;
+    const bool upper = (lane & off) != 0;  // partner holds earlier positions
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      if constexpr (RK == RK_MINMAX) {
+        const MT ob = xor_shfl<off>(best[i]);
+        const int32_t oa = xor_shfl<off>(barg[i]);
+        bool take;
+        if (nanprop) {
+          take = oa != kNone32 && (barg[i] == kNone32 || (ob != ob) || better(ob, best[i], is_min));
+        } else if (later) {
+          take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
+                                   (ob == best[i] && oa > barg[i]));
+        } else {
+          take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
+                                   (ob == best[i] && oa < barg[i]));
+        }
+        if (take) {
+          best[i] = ob;
+          barg[i] = oa;
+        }
+      } else if constexpr (RK == RK_LSE) {
+        const float om = xor_shfl<off>((float)best[i]);
+        const float os = xor_shfl<off>(acc[i]);
+        // merge in position order so every lane computes the same value
+        float m1 = upper ? om : (float)best[i], s1 = upper ? os : acc[i];
+        const float m2 = upper ? (float)best[i] : om, s2 = upper ? acc[i] : os;
+        lse_merge(m1, s1, m2, s2);
+        best[i] = m1;
+        acc[i] = s1;
+      } else {
+        const float o = xor_shfl<off>(acc[i]);
+        const float lo_v = upper ? o : acc[i], hi_v = upper ? acc[i] : o;
+        acc[i] = is_prod ? lo_v * hi_v : lo_v + hi_v;
+      }
+    }
+  };
   // Combine the S sub-group partials of the current row; all lanes end with
   // the combined state.  Lower sub-groups hold earlier positions.
   auto combine = [&]() {
-#pragma unroll
-    for (int off = G; off < kWave; off <<= 1) {
-      const bool upper = (lane & off) != 0;  // partner holds earlier positions
-#pragma unroll
-      for (int i = 0; i < NE; ++i) {
-        if constexpr (RK == RK_MINMAX) {
-          const MT ob = (MT)(sizeof(MT) == 8 ? shfld((double)best[i], lane ^ off)
-                                             : shflf((float)best[i], lane ^ off));
-          const int32_t oa = shfl32(barg[i], lane ^ off);
-          bool take;
-          if (nanprop) {
-            take = oa != kNone32 && (barg[i] == kNone32 || (ob != ob) || better(ob, best[i], is_min));
-          } else if (later) {
-            take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
-                                     (ob == best[i] && oa > barg[i]));
-          } else {
-            take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
-                                     (ob == best[i] && oa < barg[i]));
-          }
-          if (take) {
-            best[i] = ob;
-            barg[i] = oa;
-          }
-        } else if constexpr (RK == RK_LSE) {
-          const float om = shflf((float)best[i], lane ^ off);
-          const float os = shflf(acc[i], lane ^ off);
-          // merge in position order so every lane computes the same value
-          float m1 = upper ? om : (float)best[i], s1 = upper ? os : acc[i];
-          const float m2 = upper ? (float)best[i] : om, s2 = upper ? acc[i] : os;
-          lse_merge(m1, s1, m2, s2);
-          best[i] = m1;
-          acc[i] = s1;
-        } else {
-          const float o = shflf(acc[i], lane ^ off);
-          const float lo_v = upper ? o : acc[i], hi_v = upper ? acc[i] : o;
-          acc[i] = is_prod ? lo_v * hi_v : lo_v + hi_v;
-        }
-      }
-    }
+    if constexpr (G <= 1) combine_round(std::integral_constant<int, 1>{});
+    if constexpr (G <= 2) combine_round(std::integral_constant<int, 2>{});
+    if constexpr (G <= 4) combine_round(std::integral_constant<int, 4>{});
+    if constexpr (G <= 8) combine_round(std::integral_constant<int, 8>{});
+    if constexpr (G <= 16) combine_round(std::integral_constant<int, 16>{});
+    if constexpr (G <= 32) combine_round(std::integral_constant<int, 32>{});
   };
 
   auto write_record = [&](bool head) {
@@ -428,12 +440,18 @@ void engine_kernel(Params p) {
       // Doing them before any gather is issued keeps the wait for the staged
       // col/value loads ahead of the gathers, so the U gathers overlap.
       int64_t cc[kUnroll];
+      uint32_t co[kUnroll];  // OFF32: byte offset of the gathered packet
       float ws[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int idx = (j0 + u) * S + sub;
         if constexpr (GATHER) {
-          cc[u] = (int64_t)shfl64((IDX)cl, idx & (kWave - 1));
+          if constexpr (OFF32) {
+            co[u] = (uint32_t)shfl32((int32_t)cl, idx & (kWave - 1)) * (uint32_t)(K * sizeof(S_t)) +
+                    (uint32_t)(k0 * sizeof(S_t));
+          } else {
+            cc[u] = (int64_t)shfl64((IDX)cl, idx & (kWave - 1));
+          }
         } else {
           cc[u] = std::min<int64_t>(wbase + idx, p.n - 1);
         }
@@ -445,7 +463,11 @@ void engine_kernel(Params p) {
         const int idx = (j0 + u) * S + sub;
         const bool ok = (j0 + u) < nsteps && idx < nw && kok;
         if constexpr (VL) {
-          xr[u] = ok ? load16(srcb + cc[u] * K + k0) : make_uint4(0u, 0u, 0u, 0u);
+          if constexpr (OFF32) {
+            xr[u] = ok ? load16(reinterpret_cast<const char*>(srcb) + co[u]) : make_uint4(0u, 0u, 0u, 0u);
+          } else {
+            xr[u] = ok ? load16(srcb + cc[u] * K + k0) : make_uint4(0u, 0u, 0u, 0u);
+          }
 #pragma unroll
           for (int i = 0; i < NW; ++i) w[u][i] = ws[u];
           if constexpr (NW > 1) {
@@ -462,10 +484,9 @@ void engine_kernel(Params p) {
           if (val_mode == 2 && ok) w[u][0] = E::load1(val, (wbase + idx) * K + k0);
         }
       }
-      // Phase 3: consume the steps in order.  The loop is not unrolled (the
-      // row-finishing code it contains is large); the staged steps rotate
-      // down one slot per iteration so that they stay in registers.
-#pragma unroll 1
+      // Phase 3: consume the steps in order (fully unrolled, so the staged
+      // steps stay in registers).
+#pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         if (j0 + u >= nsteps) break;
         const int64_t e_first = wbase + (int64_t)(j0 + u) * S;
@@ -473,18 +494,11 @@ void engine_kernel(Params p) {
         const int64_t e_mine = e_first + sub;
         const bool valid = e_mine < hi;
         float x[NE];
-        if constexpr (VL) E::unpack(xr[0], x);
-        else x[0] = xs[0];
+        if constexpr (VL) E::unpack(xr[u], x);
+        else x[0] = xs[u];
         float wcur[NW];
 #pragma unroll
-        for (int i = 0; i < NW; ++i) wcur[i] = w[0][i];
-#pragma unroll
-        for (int t = 0; t + 1 < kUnroll; ++t) {
-          xr[t] = xr[t + 1];
-          xs[t] = xs[t + 1];
-#pragma unroll
-          for (int i = 0; i < NW; ++i) w[t][i] = w[t + 1][i];
-        }
+        for (int i = 0; i < NW; ++i) wcur[i] = w[u][i];
         bool added = false;
         while (true) {
           if (!added && valid && e_mine < re) {
@@ -707,6 +721,14 @@ inline int variant_of(int rk, bool gather, const Params& p) {
 template <int DT, typename IDX, int RK, bool GATHER>
 void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
   const int v = variant_of(RK, GATHER, p);
+  if constexpr (GATHER) {
+    // every gathered byte offset (row * K + k) * size fits in 32 bits
+    const uint64_t bytes = (uint64_t)p.n * (uint64_t)p.k * sizeof(typename Elem<DT>::S);
+    if (v == V_FIRST && pl.vec && bytes < (1ull << 32)) {
+      launch_g<DT, IDX, true, RK, GATHER, V_FIRST32>(pl.g, grid, s, p);
+      return;
+    }
+  }
   if constexpr (!GATHER && RK == RK_MINMAX) {
     if (v == V_LATER) {
       launch_rk_f<DT, IDX, RK, GATHER, V_LATER>(pl, grid, s, p);

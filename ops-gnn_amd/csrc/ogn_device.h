@@ -234,6 +234,34 @@ __device__ __forceinline__ double shfld(double v, int src) {
   return __longlong_as_double(shfl64((int64_t)__double_as_longlong(v), src));
 }
 
+// Value of lane (lane ^ OFF), OFF a power of two below 64: ds_swizzle in
+// xor mode (no address register) within 32-lane halves, ds_bpermute across
+// them.
+template <int OFF>
+__device__ __forceinline__ int32_t xor_shfl32(int32_t v) {
+  static_assert(OFF >= 1 && OFF <= 32 && (OFF & (OFF - 1)) == 0, "OFF must be a power of two <= 32");
+  if constexpr (OFF == 32) {
+    return __builtin_amdgcn_ds_bpermute((int)((threadIdx.x ^ 32) & 63) << 2, v);
+  } else {
+    return __builtin_amdgcn_ds_swizzle(v, (OFF << 10) | 0x1f);
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float xor_shfl(float v) {
+  return __int_as_float(xor_shfl32<OFF>(__float_as_int(v)));
+}
+template <int OFF>
+__device__ __forceinline__ int32_t xor_shfl(int32_t v) {
+  return xor_shfl32<OFF>(v);
+}
+template <int OFF>
+__device__ __forceinline__ double xor_shfl(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)xor_shfl32<OFF>((int32_t)(uint32_t)u);
+  const uint32_t hi = (uint32_t)xor_shfl32<OFF>((int32_t)(uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }

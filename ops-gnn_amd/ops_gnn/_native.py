@@ -164,18 +164,21 @@ class _VersionCache:
 INDEX_FACTS = _VersionCache()
 
 
-def index_facts(index: torch.Tensor) -> Tuple[bool, int, int]:
-    """(sorted, min, max) of an int64 index; one 24-byte device-to-host read,
-    cached per tensor version."""
+def index_facts(index: torch.Tensor, key: Optional[torch.Tensor] = None) -> Tuple[bool, int, int]:
+    """(sorted, min, max) of an int32 / int64 index; one 24-byte
+    device-to-host read, cached per tensor version of `key` (default: `index`
+    itself; pass the caller's tensor when `index` is a fresh view of it)."""
 
     def compute():
         idx = index.contiguous()
+        if idx.dtype != torch.int64:
+            idx = idx.to(torch.int64)
         facts = torch.empty(3, dtype=torch.int64, device=idx.device)
         check(lib.ogn_index_facts(dptr(idx), idx.numel(), dptr(facts), stream_of(idx)), "index facts")
         unsorted, mn, mx = facts.tolist()
         return (unsorted == 0, mn, mx)
 
-    return INDEX_FACTS.get(index, compute)
+    return INDEX_FACTS.get(index if key is None else key, compute)
 
 
 def scatter_atomic(src3: torch.Tensor, index: torch.Tensor, strides, size: int, reduce: int,

@@ -67,12 +67,22 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
     _lib.require_gpu(src, index, what="scatter")
     expanded = broadcast(index, src, dim)
     compact = index.dim() == 1 and index.numel() == src.size(dim)
+    line = index
+    if not compact and expanded.dim() == src.dim() and all(
+            expanded.stride(d) == 0 or expanded.size(d) == 1 for d in range(src.dim()) if d != dim):
+        # an index broadcast along every other dim (torch_scatter's usual
+        # `index.view(-1, 1).expand_as(src)`) is one 1-D vector along dim
+        line = expanded
+        for d in reversed(range(src.dim())):
+            if d != dim:
+                line = line.select(d, 0)
+        compact = line.numel() == src.size(dim)
     if out is not None:
         size = out.size(dim)
     elif dim_size is not None:
         size = int(dim_size)
     else:
-        size = (_native.index_facts(index)[2] + 1) if index.numel() else 0
+        size = (_native.index_facts(line, key=index)[2] + 1) if index.numel() else 0
     shape = list(src.shape)
     shape[dim] = size
     if out is not None:
@@ -93,14 +103,14 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
     arg3 = None
     use_segments = False
     if compact and index.numel() > 0:
-        is_sorted, mn, mx = _native.index_facts(index)
+        is_sorted, mn, mx = _native.index_facts(line, key=index)
         use_segments = is_sorted and mn >= 0 and mx < size
     if use_segments:
-        ptr = _native.ind2ptr_batched(index.reshape(1, -1), size)
+        ptr = _native.ind2ptr_batched(line.contiguous().reshape(1, -1), size)
         res3, arg3 = _native.segment_reduce(src3, ptr, size, code, _lib.SEM_SCATTER, out3, has_out, is_minmax)
     else:
         if compact:
-            idx, strides = index.contiguous(), (0, 1, 0)
+            idx, strides = line.contiguous(), (0, 1, 0)
         else:
             idx, strides = expanded.contiguous(), (length * after, after, 1)
         arg3 = _native.scatter_atomic(src3, idx, strides, size, code, out3, has_out)

@@ -40,7 +40,8 @@ def _split(shape, dim):
 
 def _pointer_facts(ptr2d: torch.Tensor):
     """(non-decreasing and >= 0, max) of a pointer tensor: one small
-    device-to-host read, cached per tensor version."""
+    device-to-host read, cached per tensor version.  Pass the caller's own
+    tensor (not a fresh view of it) so that the cache can hit."""
     def compute():
         p = ptr2d
         bad = (p < 0).any()
@@ -107,7 +108,8 @@ def _segment_csr(src, indptr, out, reduce, return_arg):
         ptr2d = indptr.reshape(1, -1).contiguous()
     else:
         ptr2d = indptr.expand(*src.shape[:dim], segs + 1).reshape(before, segs + 1).contiguous()
-    ok, top = _pointer_facts(ptr2d)
+    # broadcasting repeats pointer rows, so the facts of indptr are those of ptr2d
+    ok, top = _pointer_facts(indptr)
     if not ok:
         raise RuntimeError("indptr must be nondecreasing and non-negative")
     if top > length:

@@ -69,7 +69,7 @@ def resolve_dim_size(index: torch.Tensor, dim_size: Optional[int], facts) -> int
 def _facts(index: torch.Tensor):
     if index.numel() == 0:
         return (True, 0, -1)
-    return _native.index_facts(index.to(torch.int64) if index.dtype != torch.int64 else index)
+    return _native.index_facts(index)
 
 
 def _prepare(op, src, index, dim, dim_size):

@@ -106,6 +106,36 @@ def test_full_shape_index_and_negative_dim(ogn, oracle, reduce):
     _check(ogn, oracle, src, idx1, -1, 4, reduce, what="last dim")
 
 
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("sorted_index", [True, False])
+def test_broadcast_view_index_matches_oracle(ogn, oracle, reduce, sorted_index):
+    # torch_scatter's usual call: index.view(-1, 1).expand_as(src) -- a
+    # stride-0 view on the GPU, which takes the 1-D path (segment engine
+    # when sorted) and must give the oracle's result
+    rng = np.random.default_rng(64)
+    idx = rng.integers(0, 50, 700)
+    if sorted_index:
+        idx = np.sort(idx)
+    src = torch.from_numpy(rng.standard_normal((700, 6)).astype(np.float32))
+    fn = {"sum": ogn.scatter_sum, "mean": ogn.scatter_mean, "min": ogn.scatter_min, "max": ogn.scatter_max}[reduce]
+    dsrc = src.cuda()
+    view = torch.from_numpy(idx).cuda().view(-1, 1).expand_as(dsrc)
+    assert view.stride(1) == 0
+    res = fn(dsrc, view, 0, None, 50)
+    got, arg = res if isinstance(res, tuple) else (res, None)
+    full = torch.from_numpy(idx).view(-1, 1).expand(700, 6).contiguous()
+    gold, garg = oracle.scatter(src, full, 0, 50, reduce)
+    if reduce in ("min", "max"):
+        assert_exact(got, cast_like(gold, src.dtype), "broadcast view values")
+        assert_exact(arg, garg, "broadcast view arg")
+    else:
+        scale, _ = oracle.scatter(src.abs(), full, 0, 50, "sum")
+        if reduce == "mean":
+            cnt, _ = oracle.scatter(torch.ones_like(src), full, 0, 50, "sum")
+            scale = scale / np.maximum(cnt, 1)
+        assert_sum_close(got, gold, scale, src.dtype, "broadcast view")
+
+
 def test_scatter_dim_size_inference_and_empty(ogn):
     src = torch.randn(5, 3, device="cuda")
     out = ogn.scatter(src, torch.tensor([0, 4, 4, 1, 0], device="cuda"), dim=0)
