@@ -297,6 +297,24 @@ int ogn_group_softmax_backward(const void* saved, const void* grad, const void* 
                                int64_t groups, int mode, void* grad_src, float* workspace, size_t workspace_bytes,
                                void* stream);
 
+/* ------------------------------------------------------------------ gather
+ * Expansion of segment rows (raw bytes: any dtype, bit-exact).
+ * ogn_gather_csr: out[b, i, :] = src[b, s, :] for indptr[s] <= i < indptr[s+1]
+ *   (the last such s); rows before indptr[0] are zero.  indptr: int64
+ *   [ptr_batches, segments + 1], ptr_batches 1 (shared) or batch, each row
+ *   non-decreasing and ending at out_rows.  src [batch, segments, row_bytes],
+ *   out [batch, out_rows, row_bytes].  Replaces gather_csr (reference
+ *   csrc/npu/gather_csr/op_host/gather_csr.cpp:338, golden
+ *   test/gather_csr/arch35/golden.py:63-90).
+ * ogn_gather_coo: out[b, e, :] = src[b, index[b, e], :]; index int64
+ *   [batch, entries], values clamped into [0, src_rows).  Replaces gather_coo
+ *   (reference csrc/npu/gather_coo/op_host/gather_coo.cpp, golden
+ *   test/gather_coo/arch35/test_gather_coo.py:87-106). */
+int ogn_gather_csr(const int64_t* indptr, int64_t ptr_batches, const void* src, int64_t batch, int64_t segments,
+                   int64_t row_bytes, int64_t out_rows, void* out, void* stream);
+int ogn_gather_coo(const int64_t* index, const void* src, int64_t batch, int64_t src_rows, int64_t entries,
+                   int64_t row_bytes, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

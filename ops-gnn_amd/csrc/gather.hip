@@ -1,0 +1,158 @@
+// gather_csr / gather_coo for gfx950: expand segment rows back over their
+// positions (the inverse of a segment reduction, and its backward for sum).
+//
+//   gather_csr: out[b, i, :] = src[b, s, :] for ptr[s] <= i < ptr[s+1];
+//               rows before ptr[0] are zero.
+//   gather_coo: out[b, e, :] = src[b, index[b, e], :].
+//
+// Rows are raw bytes (any dtype, bit-exact copies, NaN payloads kept).  A
+// block owns a tile of 64 output rows: one thread per row finds its source
+// row (a branch-free upper_bound over the pointer row for CSR, a load for
+// COO) into LDS, then the block copies the tile's packets -- 16, 8, 4, 2 or
+// 1 bytes each, the widest that divides the row and both base addresses --
+// with consecutive threads on consecutive packets, so reads of one source
+// row and writes of the tile are coalesced.
+#include "ogn_device.h"
+
+#include <algorithm>
+
+namespace ogn {
+namespace {
+
+constexpr int kTileRows = 64;
+constexpr int kThreads = 256;
+
+struct GatherArgs {
+  const int64_t* ptr;    // csr: [ptr_batches, segments + 1]
+  const int64_t* index;  // coo: [batch, entries]
+  int64_t ptr_bstride;   // 0 when one pointer row is shared
+  const char* src;       // [batch, src_rows, row_bytes]
+  char* out;             // [batch, out_rows, row_bytes]
+  int64_t src_rows, out_rows, row_bytes;
+  FastDiv ppr;           // packets per row
+};
+
+template <int P>
+struct Packet;
+template <> struct Packet<16> { using T = uint4; };
+template <> struct Packet<8> { using T = uint2; };
+template <> struct Packet<4> { using T = uint32_t; };
+template <> struct Packet<2> { using T = uint16_t; };
+template <> struct Packet<1> { using T = uint8_t; };
+
+template <int P, bool CSR>
+__global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
+  using T = typename Packet<P>::T;
+  __shared__ int64_t rows[kTileRows];
+  const int64_t b = blockIdx.y;
+  const int64_t i0 = (int64_t)blockIdx.x * kTileRows;
+  const int64_t nrows = std::min<int64_t>(kTileRows, a.out_rows - i0);
+  if (threadIdx.x < nrows) {
+    const int64_t i = i0 + threadIdx.x;
+    int64_t s;
+    if constexpr (CSR) {
+      // last s with ptr[s] <= i (segments = src_rows); -1 before ptr[0]
+      const int64_t* ptr = a.ptr + b * a.ptr_bstride;
+      int64_t lo = 0, n = a.src_rows + 1;  // search ptr[0 .. segments]
+      while (n > 0) {
+        const int64_t half = n >> 1;
+        const bool right = ptr[lo + half] <= i;
+        lo = right ? lo + half + 1 : lo;
+        n = right ? n - half - 1 : half;
+      }
+      s = lo - 1;  // number of entries <= i, minus one
+      if (s >= a.src_rows) s = -1;  // past the last segment end (not produced)
+    } else {
+      s = a.index[b * a.out_rows + i];
+      s = std::min<int64_t>(std::max<int64_t>(s, 0), a.src_rows - 1);
+    }
+    rows[threadIdx.x] = s;
+  }
+  __syncthreads();
+  const int64_t ppr = (int64_t)a.ppr.d;
+  const int64_t total = nrows * ppr;
+  const T* __restrict__ src = reinterpret_cast<const T*>(a.src + b * a.src_rows * a.row_bytes);
+  T* __restrict__ out = reinterpret_cast<T*>(a.out + (b * a.out_rows + i0) * a.row_bytes);
+  for (int64_t p = threadIdx.x; p < total; p += kThreads) {
+    const int64_t r = fdiv(p, a.ppr);
+    const int64_t q = p - r * ppr;
+    const int64_t s = rows[r];
+    T v;
+    if (s >= 0) {
+      v = src[s * ppr + q];
+    } else {
+      v = T{};
+    }
+    out[r * ppr + q] = v;
+  }
+}
+
+int packet_for(const void* src, const void* out, int64_t row_bytes) {
+  for (int p : {16, 8, 4, 2}) {
+    if (row_bytes % p == 0 && (uintptr_t)src % p == 0 && (uintptr_t)out % p == 0) return p;
+  }
+  return 1;
+}
+
+template <bool CSR>
+int launch(GatherArgs& a, int64_t batch, const void* src, void* out, hipStream_t s, const char* name) {
+  const int p = packet_for(src, out, a.row_bytes);
+  a.ppr = make_fastdiv(a.row_bytes / p);
+  const dim3 grid((unsigned)((a.out_rows + kTileRows - 1) / kTileRows), (unsigned)batch);
+  TimedLaunch t(name, s);
+  switch (p) {
+    case 16: hipLaunchKernelGGL((gather_kernel<16, CSR>), grid, dim3(kThreads), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((gather_kernel<8, CSR>), grid, dim3(kThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((gather_kernel<4, CSR>), grid, dim3(kThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((gather_kernel<2, CSR>), grid, dim3(kThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((gather_kernel<1, CSR>), grid, dim3(kThreads), 0, s, a); break;
+  }
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace ogn
+
+using namespace ogn;
+
+extern "C" {
+
+int ogn_gather_csr(const int64_t* indptr, int64_t ptr_batches, const void* src, int64_t batch, int64_t segments,
+                   int64_t row_bytes, int64_t out_rows, void* out, void* stream) {
+  if (ptr_batches < 0 || batch < 0 || segments < 0 || row_bytes < 0 || out_rows < 0)
+    return fail(OGN_EINVAL, "ogn_gather_csr: negative size");
+  if (batch == 0 || out_rows == 0 || row_bytes == 0) return OGN_OK;
+  if (ptr_batches != 1 && ptr_batches != batch)
+    return fail(OGN_EINVAL, "ogn_gather_csr: ptr_batches must be 1 or batch");
+  if (batch > 65535) return fail(OGN_EUNSUPPORTED, "ogn_gather_csr: batch > 65535");
+  if (!indptr || !out || (segments > 0 && !src)) return fail(OGN_EINVAL, "ogn_gather_csr: null pointer");
+  GatherArgs a{};
+  a.ptr = indptr;
+  a.ptr_bstride = ptr_batches == 1 ? 0 : segments + 1;
+  a.src = static_cast<const char*>(src);
+  a.out = static_cast<char*>(out);
+  a.src_rows = segments;
+  a.out_rows = out_rows;
+  a.row_bytes = row_bytes;
+  return launch<true>(a, batch, src, out, static_cast<hipStream_t>(stream), "gather_csr");
+}
+
+int ogn_gather_coo(const int64_t* index, const void* src, int64_t batch, int64_t src_rows, int64_t entries,
+                   int64_t row_bytes, void* out, void* stream) {
+  if (batch < 0 || src_rows < 0 || entries < 0 || row_bytes < 0)
+    return fail(OGN_EINVAL, "ogn_gather_coo: negative size");
+  if (batch == 0 || entries == 0 || row_bytes == 0) return OGN_OK;
+  if (src_rows == 0) return fail(OGN_EINVAL, "ogn_gather_coo: entries need a non-empty src");
+  if (batch > 65535) return fail(OGN_EUNSUPPORTED, "ogn_gather_coo: batch > 65535");
+  if (!index || !src || !out) return fail(OGN_EINVAL, "ogn_gather_coo: null pointer");
+  GatherArgs a{};
+  a.index = index;
+  a.src = static_cast<const char*>(src);
+  a.out = static_cast<char*>(out);
+  a.src_rows = src_rows;
+  a.out_rows = entries;
+  a.row_bytes = row_bytes;
+  return launch<false>(a, batch, src, out, static_cast<hipStream_t>(stream), "gather_coo");
+}
+
+}  // extern "C"

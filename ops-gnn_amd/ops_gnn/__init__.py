@@ -26,6 +26,7 @@ from .scatter import (
 from .softmax import scatter_softmax, scatter_log_softmax, scatter_logsumexp
 from .sddmm_csr import sddmm_csr
 from .spmm import spmm, bspmm
+from .gather import gather_csr, gather_coo
 
 __version__ = "0.1.0"
 
@@ -47,4 +48,5 @@ __all__ = [
     "scatter", "scatter_sum", "scatter_add", "scatter_mul", "scatter_mean", "scatter_min", "scatter_max",
     "scatter_softmax", "scatter_log_softmax", "scatter_logsumexp",
     "sddmm_csr", "spmm", "bspmm",
+    "gather_csr", "gather_coo",
 ]

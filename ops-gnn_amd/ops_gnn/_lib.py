@@ -76,6 +76,8 @@ SIGNATURES = {
     "ogn_group_softmax_apply": (_int, [_vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _int,
                                        _vp]),
     "ogn_group_lse_from_stats": (_int, [_vp, _vp, _i64, _vp, _int, _vp]),
+    "ogn_gather_csr": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "ogn_gather_coo": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "ogn_group_softmax_backward": (_int, [_vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _int, _vp,
                                           _vp, _sz, _vp]),
 }

@@ -489,3 +489,28 @@ void oracle_spmm_dgl(const int64_t* ptr, const int64_t* col, int64_t m, const fl
     }
   }
 }
+
+/* ---------------------------------------------------------------- gather
+ * reference test/gather_csr/arch35/golden.py:63-90 (gather_csr_cpu): out row
+ * i of batch b is src row s with ptr[s] <= i < ptr[s+1], rows before ptr[0]
+ * stay zero; rows are copied as raw bytes.  gather_coo
+ * (test/gather_coo/arch35/test_gather_coo.py:87-106): out[b, e] = src[b, index[b, e]].
+ */
+void oracle_gather_csr(const int64_t* ptr, int64_t ptr_batches, const unsigned char* src, int64_t batch,
+                       int64_t segments, int64_t row_bytes, int64_t out_rows, unsigned char* out) {
+  memset(out, 0, (size_t)(batch * out_rows * row_bytes));
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t* p = ptr + (ptr_batches == 1 ? 0 : b) * (segments + 1);
+    for (int64_t s = 0; s < segments; ++s)
+      for (int64_t i = p[s]; i < p[s + 1]; ++i)
+        memcpy(out + (b * out_rows + i) * row_bytes, src + (b * segments + s) * row_bytes, (size_t)row_bytes);
+  }
+}
+
+void oracle_gather_coo(const int64_t* index, const unsigned char* src, int64_t batch, int64_t src_rows,
+                       int64_t entries, int64_t row_bytes, unsigned char* out) {
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t e = 0; e < entries; ++e)
+      memcpy(out + (b * entries + e) * row_bytes, src + (b * src_rows + index[b * entries + e]) * row_bytes,
+             (size_t)row_bytes);
+}

@@ -54,6 +54,9 @@ def lib():
                                      ctypes.c_double, _f64p, vp]
         l.oracle_segment_lse.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, _f64p]
         l.oracle_group_softmax.argtypes = [_f32p, _i64p, i64, i64, i64, i64, ctypes.c_int, _f64p]
+        u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+        l.oracle_gather_csr.argtypes = [_i64p, i64, u8p, i64, i64, i64, i64, u8p]
+        l.oracle_gather_coo.argtypes = [_i64p, u8p, i64, i64, i64, i64, u8p]
         l.oracle_group_softmax_backward.argtypes = [_f32p, _f32p, _i64p, i64, i64, i64, i64, ctypes.c_int,
                                                     _f64p]
         l.oracle_sddmm.argtypes = [_i64p, _i64p, i64, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, i64,
@@ -296,3 +299,59 @@ def spmm_dgl(ptr, col, x, rhs, op, reduce):
 
 def threads() -> int:
     return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def _raw(t):
+    """numpy view of a tensor / array as raw bytes (C order) and its dtype."""
+    import torch
+
+    if isinstance(t, torch.Tensor):
+        t = t.detach().cpu().contiguous()
+        return t.view(torch.uint8).numpy().reshape(-1), t.dtype
+    a = np.ascontiguousarray(t)
+    return a.view(np.uint8).reshape(-1), a.dtype
+
+
+def gather_csr(src, indptr):
+    """reference test/gather_csr/arch35/golden.py:63-90; returns a torch CPU tensor."""
+    import torch
+
+    src_t = src if isinstance(src, torch.Tensor) else torch.from_numpy(np.asarray(src))
+    ptr = _np(indptr, np.int64)
+    dim = ptr.ndim - 1
+    before = int(np.prod(src_t.shape[:dim])) if dim else 1
+    width = ptr.shape[-1]
+    ptr2 = np.ascontiguousarray(np.broadcast_to(ptr, tuple(src_t.shape[:dim]) + (width,)).reshape(-1, width))
+    segs = width - 1
+    rows = int(ptr2[0, -1]) if ptr2.size else 0
+    feat = int(np.prod(src_t.shape[dim + 1:])) if src_t.dim() > dim + 1 else 1
+    shape = list(src_t.shape)
+    shape[dim] = rows
+    out = torch.zeros(shape, dtype=src_t.dtype)
+    if out.numel() == 0 or segs <= 0:
+        return out
+    raw, _ = _raw(src_t)
+    ob = np.zeros(out.numel() * out.element_size(), np.uint8)
+    lib().oracle_gather_csr(ptr2, ptr2.shape[0], raw, before, segs, feat * src_t.element_size(), rows, ob)
+    return torch.from_numpy(ob).view(src_t.dtype).reshape(shape)
+
+
+def gather_coo(src, index):
+    """reference test/gather_coo/arch35/test_gather_coo.py:87-106; torch CPU tensor."""
+    import torch
+
+    src_t = src if isinstance(src, torch.Tensor) else torch.from_numpy(np.asarray(src))
+    idx = np.ascontiguousarray(_np(index, np.int64))
+    dim = idx.ndim - 1
+    before = int(np.prod(src_t.shape[:dim])) if dim else 1
+    feat = int(np.prod(src_t.shape[dim + 1:])) if src_t.dim() > dim + 1 else 1
+    shape = list(src_t.shape)
+    shape[dim] = idx.shape[-1]
+    out = torch.zeros(shape, dtype=src_t.dtype)
+    if out.numel() == 0:
+        return out
+    raw, _ = _raw(src_t)
+    ob = np.zeros(out.numel() * out.element_size(), np.uint8)
+    lib().oracle_gather_coo(idx.reshape(-1), raw, before, src_t.size(dim), idx.shape[-1],
+                            feat * src_t.element_size(), ob)
+    return torch.from_numpy(ob).view(src_t.dtype).reshape(shape)

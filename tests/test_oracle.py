@@ -529,3 +529,46 @@ def test_group_softmax_backward_special_values_follow_torch():
         ref = t.grad.numpy()
         np.testing.assert_array_equal(np.isnan(got), np.isnan(ref), err_msg=mode)
         np.testing.assert_allclose(got[~np.isnan(ref)], ref[~np.isnan(ref)], rtol=1e-12, err_msg=mode)
+
+
+# ----------------------------------------------------------------- gather_csr / gather_coo
+# reference test/gather_csr/arch35/golden.py:23-51 (CASES: src, coo index, indptr, expected)
+GATHER_CASES = [
+    ([1, 2, 3, 4], [0, 0, 1, 1, 1, 3], [0, 2, 5, 5, 6], [1, 1, 2, 2, 2, 4]),
+    ([[1, 2], [3, 4], [5, 6], [7, 8]], [0, 0, 1, 1, 1, 3], [0, 2, 5, 5, 6],
+     [[1, 2], [1, 2], [3, 4], [3, 4], [3, 4], [7, 8]]),
+    ([[1, 3, 5, 7], [2, 4, 6, 8]], [[0, 0, 1, 1, 1, 3], [0, 0, 0, 1, 1, 2]],
+     [[0, 2, 5, 5, 6], [0, 3, 5, 6, 6]], [[1, 1, 3, 3, 3, 7], [2, 2, 2, 4, 4, 6]]),
+    ([[[1, 2], [3, 4], [5, 6]], [[7, 9], [10, 11], [12, 13]]], [[0, 0, 1], [0, 2, 2]],
+     [[0, 2, 3, 3], [0, 1, 1, 3]], [[[1, 2], [1, 2], [3, 4]], [[7, 9], [12, 13], [12, 13]]]),
+    ([[1], [2]], [[0, 0], [0, 0]], [[0, 2], [0, 2]], [[1, 1], [2, 2]]),
+    ([[[1, 1]], [[2, 2]]], [[0, 0], [0, 0]], [[0, 2], [0, 2]], [[[1, 1], [1, 1]], [[2, 2], [2, 2]]]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(GATHER_CASES)))
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32, torch.float64, torch.int32,
+                                   torch.int64])
+def test_gather_official_cases(case, dtype):
+    src, coo, ptr, expected = GATHER_CASES[case]
+    s = torch.tensor(src).to(dtype)
+    want = torch.tensor(expected).to(dtype)
+    assert torch.equal(orc.gather_csr(s, np.array(ptr)), want)
+    assert torch.equal(orc.gather_coo(s, np.array(coo)), want)
+
+
+def test_gather_csr_uncovered_prefix_kat():
+    # reference test/gather_csr/arch35/test_gather_csr.py:278-283
+    got = orc.gather_csr(torch.tensor([3, 5], dtype=torch.int32), np.array([2, 4, 6]))
+    assert torch.equal(got, torch.tensor([0, 0, 3, 3, 5, 5], dtype=torch.int32))
+
+
+def test_gather_matches_repeat_interleave_and_index_select():
+    rng = np.random.default_rng(16)
+    lengths = rng.integers(0, 5, 40)
+    ptr = np.concatenate([[0], np.cumsum(lengths)])
+    src = torch.from_numpy(rng.standard_normal((40, 7)))
+    want = src.repeat_interleave(torch.from_numpy(lengths), dim=0)
+    assert torch.equal(orc.gather_csr(src, ptr), want)
+    idx = np.repeat(np.arange(40), lengths)
+    assert torch.equal(orc.gather_coo(src, idx), src.index_select(0, torch.from_numpy(idx)))
