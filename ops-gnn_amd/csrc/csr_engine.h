@@ -402,7 +402,7 @@ void engine_kernel(Params p) {
                             barg[i] == kNone32 ? kNone : lo + barg[i], &v[i], &ag[i]);
       const int64_t off = b * p.out_bstride + r * K + k0;
       if (VL || k0 + NE <= K) {
-        store_floats<NE>(p.out, p.out_dt, off, v);
+        store_floats<NE, true>(p.out, p.out_dt, off, v);
       }
       if constexpr (RK == RK_MINMAX) {
         if (p.arg) {
@@ -415,18 +415,27 @@ void engine_kernel(Params p) {
     reset();
   };
 
-  for (int64_t wbase = lo; wbase < hi; wbase += kWave) {
-    const int64_t el = wbase + lane;
+  // Column indices and weights of the next 64-position window are loaded
+  // one window ahead, so a window's gathers never wait for its staging load.
+  int64_t cl_next = 0;
+  float vl_next = 1.f;
+  auto stage = [&](int64_t wb2) {
+    const int64_t el = wb2 + lane;
     const bool ev = el < hi;
+    if constexpr (GATHER) cl_next = ev ? (int64_t)load_stream(col + el) : 0;
+    if (val_mode == 1) vl_next = ev ? E::load1(val, el) : 0.f;
+  };
+  stage(lo);
+  for (int64_t wbase = lo; wbase < hi; wbase += kWave) {
     int64_t cl;
     if constexpr (GATHER) {
-      cl = ev ? (int64_t)load_stream(col + el) : 0;
+      cl = cl_next;
     } else {
-      cl = el;
+      cl = wbase + lane;
     }
     cl = std::min<int64_t>(std::max<int64_t>(cl, 0), p.n - 1);
-    float vl = 1.f;
-    if (val_mode == 1) vl = ev ? E::load1(val, el) : 0.f;
+    const float vl = vl_next;
+    if (wbase + kWave < hi) stage(wbase + kWave);
     const int nw = (int)std::min<int64_t>(kWave, hi - wbase);
     const int nsteps = (nw + S - 1) / S;
     for (int j0 = 0; j0 < nsteps; j0 += kUnroll) {

@@ -159,15 +159,20 @@ __host__ __device__ constexpr int dtype_size(int dt) {
 // Store n consecutive fp32 values into an output of runtime dtype `dt`
 // (fp32/fp16/bf16) at element offset `off`.  `aligned` promises that the
 // address is n*size aligned so that one wide store can be used.
-template <int N>
+// NT = non-temporal stores (streaming outputs that are not read back soon).
+template <int N, bool NT = false>
 __device__ __forceinline__ void store_floats(void* out, int dt, int64_t off,
                                              const float* v) {
   if (dt == OGN_F32) {
     float* p = static_cast<float*>(out) + off;
     if constexpr (N % 4 == 0) {
 #pragma unroll
-      for (int i = 0; i < N; i += 4)
-        *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+      for (int i = 0; i < N; i += 4) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4 q = {v[i], v[i + 1], v[i + 2], v[i + 3]};
+        if constexpr (NT) __builtin_nontemporal_store(q, reinterpret_cast<f32x4*>(p + i));
+        else *reinterpret_cast<f32x4*>(p + i) = q;
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < N; ++i) p[i] = v[i];
@@ -180,10 +185,13 @@ __device__ __forceinline__ void store_floats(void* out, int dt, int64_t off,
       h[i] = dt == OGN_F16 ? f32_to_f16_bits(v[i]) : f32_to_bf16_bits(v[i]);
     if constexpr (N % 8 == 0) {
 #pragma unroll
-      for (int i = 0; i < N; i += 8)
-        *reinterpret_cast<uint4*>(p + i) = make_uint4(
-            h[i] | ((uint32_t)h[i + 1] << 16), h[i + 2] | ((uint32_t)h[i + 3] << 16),
-            h[i + 4] | ((uint32_t)h[i + 5] << 16), h[i + 6] | ((uint32_t)h[i + 7] << 16));
+      for (int i = 0; i < N; i += 8) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 q = {h[i] | ((uint32_t)h[i + 1] << 16), h[i + 2] | ((uint32_t)h[i + 3] << 16),
+                         h[i + 4] | ((uint32_t)h[i + 5] << 16), h[i + 6] | ((uint32_t)h[i + 7] << 16)};
+        if constexpr (NT) __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(p + i));
+        else *reinterpret_cast<u32x4*>(p + i) = q;
+      }
     } else if constexpr (N % 4 == 0) {
 #pragma unroll
       for (int i = 0; i < N; i += 4)
