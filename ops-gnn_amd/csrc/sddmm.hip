@@ -212,6 +212,131 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   }
 }
 
+// Sum over the G lanes of a sub-group (G a power of two, lanes aligned to
+// G); every lane of the sub-group ends with the same value.  Within 16-lane
+// rows DPP permutes do it without the LDS unit: xor 1 and xor 2 by quad
+// permutation, then the half-row and row mirrors pair each lane with one in
+// the other half; wider groups add swizzle / bpermute rounds.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (G >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if constexpr (G >= 16) v += dpp(v, std::integral_constant<int, 0x140>{}); // row_mirror
+  if constexpr (G >= 32) v += xor_shfl<16>(v);
+  if constexpr (G >= 64) v += xor_shfl<32>(v);
+  return v;
+}
+
+// dot(lhs[row(e)], rhs[col(e)]) -- the GAT score and the SpMM edge-weight
+// gradient.  Specialises the generic kernel for that case: the lhs row is
+// held in registers and reloaded only when a sub-group's row changes, rhs
+// rows are gathered U at a time with 32-bit byte offsets from a uniform
+// base, the sub-group reduction uses DPP, and column indices of the next
+// window are loaded one window ahead.
+template <int DT, typename IDX, int G>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4)))
+void sddmm_dot_kernel(SddmmParams p) {
+  using E = Elem<DT>;
+  using S_t = typename E::S;
+  constexpr int NE = E::VEC;
+  constexpr int S = kWave / G;
+  constexpr int U = 8;
+  const int lane = lane_id();
+  const int sub = lane / G;
+  const int gl = lane % G;
+  const int64_t c = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (c >= p.nchunks) return;
+  const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr);
+  const IDX* __restrict__ col = static_cast<const IDX*>(p.col);
+  const char* __restrict__ lhs = static_cast<const char*>(p.lhs);
+  const char* __restrict__ rhs = static_cast<const char*>(p.rhs);
+  const uint32_t row_bytes = (uint32_t)(p.k * sizeof(S_t));
+  const uint32_t k_off = (uint32_t)(gl * NE * sizeof(S_t));
+  const int64_t M = p.m;
+  const int64_t lo = c * p.chunk;
+  const int64_t hi = std::min(lo + p.chunk, p.nnz);
+
+  int64_t r = std::min<int64_t>(std::max<int64_t>(p.chunk_row[c], 0), std::max<int64_t>(M - 1, 0));
+  int64_t wb = r;
+  IDX pw = ptr[std::min<int64_t>(wb + 1 + lane, M)];
+  auto rowend = [&](int64_t rr) -> int64_t {
+    if (rr >= M) return kNoRow;
+    if (rr - wb >= kWave) {
+      wb = rr;
+      pw = ptr[std::min<int64_t>(wb + 1 + lane, M)];
+    }
+    return (int64_t)readlane64(pw, (int)(rr - wb));
+  };
+  int64_t re = rowend(r);
+
+  int64_t held = -1;
+  uint4 keep = make_uint4(0u, 0u, 0u, 0u);
+  int32_t cl_next = 0;
+  auto stage = [&](int64_t w) {
+    const int64_t el = w + lane;
+    cl_next = el < hi ? (int32_t)load_stream(col + el) : 0;
+  };
+  stage(lo);
+  for (int64_t wbase = lo; wbase < hi; wbase += kWave) {
+    const int32_t cl = std::min<int32_t>(std::max<int32_t>(cl_next, 0), (int32_t)(p.rhs_rows - 1));
+    if (wbase + kWave < hi) stage(wbase + kWave);
+    const int nw = (int)std::min<int64_t>(kWave, hi - wbase);
+    const int nsteps = (nw + S - 1) / S;
+    for (int j0 = 0; j0 < nsteps; j0 += U) {
+      int64_t row[U];
+      uint32_t co[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int idx = (j0 + u) * S + sub;
+        co[u] = (uint32_t)shfl32(cl, idx & (kWave - 1)) * row_bytes + k_off;
+        row[u] = 0;
+        if (j0 + u >= nsteps) continue;
+        const int64_t e_first = wbase + (int64_t)(j0 + u) * S;
+        const int64_t last = std::min<int64_t>(e_first + S, hi) - 1;
+        const int64_t e_mine = e_first + sub;
+        bool got = false;
+        while (true) {
+          if (!got && e_mine < re) {
+            row[u] = r;
+            got = true;
+          }
+          if (last < re) break;
+          ++r;
+          re = rowend(r);
+        }
+      }
+      uint4 xr[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int idx = (j0 + u) * S + sub;
+        const bool ok = (j0 + u) < nsteps && idx < nw;
+        xr[u] = ok ? load16(rhs + co[u]) : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int idx = (j0 + u) * S + sub;
+        const bool ok = (j0 + u) < nsteps && idx < nw;
+        if (ok && row[u] != held) {  // rare: a new row for this sub-group
+          held = row[u];
+          keep = held < p.lhs_rows ? load16(lhs + (uint64_t)held * row_bytes + k_off) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        float xl[NE], xv[NE];
+        E::unpack(keep, xl);
+        E::unpack(xr[u], xv);
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) d = __builtin_fmaf(xl[i], xv[i], d);
+        d = group_sum<G>(d);
+        if (gl == 0 && ok) store_floats<1>(p.out, p.dt, wbase + idx, &d);
+      }
+    }
+  }
+}
+
 template <int DT, typename IDX>
 void launch(bool vec, int g, dim3 grid, hipStream_t s, const SddmmParams& p) {
   if (!vec) {
@@ -225,6 +350,17 @@ void launch(bool vec, int g, dim3 grid, hipStream_t s, const SddmmParams& p) {
   switch (g) {
 #define OGN_G(GV) \
   case GV: hipLaunchKernelGGL((sddmm_kernel<DT, IDX, GV, true>), grid, dim3(kBlock), 0, s, p); break;
+    OGN_G(1) OGN_G(2) OGN_G(4) OGN_G(8) OGN_G(16) OGN_G(32) OGN_G(64)
+#undef OGN_G
+    default: break;
+  }
+}
+
+template <int DT, typename IDX>
+void launch_dot(int g, dim3 grid, hipStream_t s, const SddmmParams& p) {
+  switch (g) {
+#define OGN_G(GV) \
+  case GV: hipLaunchKernelGGL((sddmm_dot_kernel<DT, IDX, GV>), grid, dim3(kBlock), 0, s, p); break;
     OGN_G(1) OGN_G(2) OGN_G(4) OGN_G(8) OGN_G(16) OGN_G(32) OGN_G(64)
 #undef OGN_G
     default: break;
@@ -321,6 +457,16 @@ int ogn_sddmm_csr(const void* rowptr, const void* col, int index_dtype, int64_t 
   }
   const dim3 grid((unsigned)((pl.nchunks + kWaves - 1) / kWaves));
   TimedLaunch t("sddmm_main", s);
+  // dot(lhs[row], rhs[col]) with vector rows and 32-bit offsets -> the specialised kernel
+  const uint64_t rbytes = (uint64_t)rhs_rows * (uint64_t)k * (uint64_t)dtype_size(dtype);
+  if (op == SD_DOT && lhs_target == 0 && rhs_target == 2 && pl.vec && rbytes < (1ull << 32) && rhs_rows > 0) {
+    switch (dtype) {
+      case OGN_F32: i64 ? launch_dot<OGN_F32, int64_t>(pl.g, grid, s, p) : launch_dot<OGN_F32, int32_t>(pl.g, grid, s, p); break;
+      case OGN_F16: i64 ? launch_dot<OGN_F16, int64_t>(pl.g, grid, s, p) : launch_dot<OGN_F16, int32_t>(pl.g, grid, s, p); break;
+      default: i64 ? launch_dot<OGN_BF16, int64_t>(pl.g, grid, s, p) : launch_dot<OGN_BF16, int32_t>(pl.g, grid, s, p); break;
+    }
+    return check_launch("ogn_sddmm_csr");
+  }
   switch (dtype) {
     case OGN_F32: i64 ? launch<OGN_F32, int64_t>(pl.vec, pl.g, grid, s, p) : launch<OGN_F32, int32_t>(pl.vec, pl.g, grid, s, p); break;
     case OGN_F16: i64 ? launch<OGN_F16, int64_t>(pl.vec, pl.g, grid, s, p) : launch<OGN_F16, int32_t>(pl.vec, pl.g, grid, s, p); break;
