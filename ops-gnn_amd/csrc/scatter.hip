@@ -236,6 +236,56 @@ __global__ __launch_bounds__(256) void group_apply_kernel(GroupArgs a) {
   }
 }
 
+// One position per element (after == 1, the per-edge score layout): each
+// thread takes one 16-byte packet of consecutive positions, their groups
+// from the index and m / s per position (neighbouring positions usually
+// share a group, so those reads hit the cache).
+template <int DT>
+__global__ __launch_bounds__(256) void group_apply_rows_kernel(GroupArgs a) {
+  using E = Elem<DT>;
+  constexpr int NE = E::VEC;
+  const int64_t packets = a.before * a.len / NE;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const typename E::S* __restrict__ src = static_cast<const typename E::S*>(a.src);
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < packets; p += stride) {
+    const int64_t i0 = p * NE;
+    const int64_t b = fdiv(i0, a.sp.len);
+    const int64_t l0 = i0 - b * a.len;
+    float x[NE], v[NE];
+    E::unpack(load16(src + i0), x);
+    int64_t g[NE];
+    if (a.idx64) {
+      const int64_t* ix = static_cast<const int64_t*>(a.index) + l0;
+#pragma unroll
+      for (int j = 0; j < NE; j += 2) {
+        const longlong2 q = *reinterpret_cast<const longlong2*>(ix + j);
+        g[j] = q.x;
+        g[j + 1] = q.y;
+      }
+    } else {
+      const int32_t* ix = static_cast<const int32_t*>(a.index) + l0;
+#pragma unroll
+      for (int j = 0; j < NE; j += 4) {
+        const int4 q = *reinterpret_cast<const int4*>(ix + j);
+        g[j] = q.x;
+        g[j + 1] = q.y;
+        g[j + 2] = q.z;
+        g[j + 3] = q.w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+      if (g[j] >= 0 && g[j] < a.groups) {
+        const int64_t o = b * a.groups + g[j];
+        v[j] = group_apply_one(a, x[j], a.m[o], a.s[o]);
+      } else {
+        v[j] = 0.f;
+      }
+    }
+    store_floats<NE>(a.out, DT, i0, v);
+  }
+}
+
 // The same, one 16-byte packet of src / out per thread (4 fp32 or 8 fp16 /
 // bf16 features of one position) when after is a multiple of the packet:
 // the index and the (b, l) split are read once per packet and m / s come in
@@ -522,7 +572,14 @@ int ogn_group_softmax_apply(const void* src, int dtype, const void* index, int i
   const int ne = 16 / dtype_size(dtype);
   const bool vec = after % ne == 0 && (uintptr_t)src % 16 == 0 && (uintptr_t)out % 16 == 0 &&
                    (uintptr_t)m % 16 == 0 && (uintptr_t)s % 16 == 0;
-  if (vec) {
+  const bool rows_vec = after == 1 && len % ne == 0 && (uintptr_t)src % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                        (uintptr_t)index % 16 == 0;
+  if (rows_vec) {
+    const dim3 g(grid_for(total / ne));
+    if (dtype == OGN_F32) hipLaunchKernelGGL(group_apply_rows_kernel<OGN_F32>, g, dim3(256), 0, st, a);
+    else if (dtype == OGN_F16) hipLaunchKernelGGL(group_apply_rows_kernel<OGN_F16>, g, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(group_apply_rows_kernel<OGN_BF16>, g, dim3(256), 0, st, a);
+  } else if (vec) {
     const dim3 g(grid_for(total / ne));
     if (dtype == OGN_F32) hipLaunchKernelGGL(group_apply_vec_kernel<OGN_F32>, g, dim3(256), 0, st, a);
     else if (dtype == OGN_F16) hipLaunchKernelGGL(group_apply_vec_kernel<OGN_F16>, g, dim3(256), 0, st, a);
