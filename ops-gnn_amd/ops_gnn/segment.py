@@ -22,6 +22,7 @@ _REDUCE_OPS = ("sum", "add", "mean", "min", "max")
 _CODE = {"sum": _lib.R_SUM, "add": _lib.R_SUM, "mean": _lib.R_MEAN, "min": _lib.R_MIN, "max": _lib.R_MAX}
 
 _PTR_FACTS = _native._VersionCache()
+_LSE_FACTS = _native._VersionCache()
 
 
 def _check_reduce(reduce: str) -> None:
@@ -283,8 +284,13 @@ def segment_logsumexp(src: torch.Tensor, indptr: torch.Tensor, out: Optional[tor
     if indptr.numel() < 1:
         raise ValueError("indptr must contain at least one boundary")
     ptr = indptr.to(torch.int64).contiguous()
-    flags = torch.stack(((ptr < 0).any().to(torch.int64), (ptr[1:] < ptr[:-1]).any().to(torch.int64),
-                         ptr[-1])).cpu()
+
+    def compute():
+        # the reference reads these back on every call (segment_logsumexp.py:75-84);
+        # here once per indptr version
+        return tuple(int(v) for v in torch.stack(((ptr < 0).any().to(torch.int64),
+                                                  (ptr[1:] < ptr[:-1]).any().to(torch.int64), ptr[-1])).tolist())
+    flags = _LSE_FACTS.get(indptr, compute)
     if int(flags[0]):
         raise ValueError("indptr must be non-negative")
     if int(flags[1]):
