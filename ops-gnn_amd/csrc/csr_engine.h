@@ -129,13 +129,14 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, float om, float os
 }
 
 __device__ __forceinline__ void lse_add(float& m, float& s, float x) {
-  if (x > m) {
-    const float cn = clampf_max(x);
-    s = (s == 0.f ? 0.f : s * fast_exp(clampf_max(m) - cn)) + fast_exp(x - cn);
-    m = x;
-  } else {
-    s += fast_exp(x - clampf_max(m));
-  }
+  // Branch-free online update (lanes of a wave rarely agree on a new max):
+  // nm = max(m, x) ignores NaN, so a NaN x leaves m and turns s into NaN;
+  // +inf makes s infinite; -inf adds exp(-inf) = 0.  m never becomes NaN,
+  // so the rescale factor exp(clamp(m) - clamp(nm)) lies in [0, 1].
+  const float nm = fmaxf(m, x);
+  const float cn = clampf_max(nm);
+  s = __builtin_fmaf(s, fast_exp(clampf_max(m) - cn), fast_exp(x - cn));
+  m = nm;
 }
 
 // Finish one output element from its combined partial state.
