@@ -343,10 +343,8 @@ void engine_kernel(Params p) {
           take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
                                    (ob == best[i] && oa < barg[i]));
         }
-        if (take) {
-          best[i] = ob;
-          barg[i] = oa;
-        }
+        best[i] = take ? ob : best[i];
+        barg[i] = take ? oa : barg[i];
       } else if constexpr (RK == RK_LSE) {
         const float om = xor_shfl<off>((float)best[i]);
         const float os = xor_shfl<off>(acc[i]);
@@ -518,19 +516,14 @@ void engine_kernel(Params p) {
               const float wi = wcur[NW > 1 ? i : 0];
               if constexpr (RK == RK_MINMAX) {
                 const MT pv = apply_op<MT>((MT)x[i], (MT)wi, vop);
-                if (nanprop) {
-                  if (barg[i] == kNone32 || (pv != pv) || better(pv, best[i], is_min)) {
-                    best[i] = pv;
-                    barg[i] = (int32_t)(e_mine - lo);
-                  }
-                } else if (!(pv != pv)) {
-                  const bool take = barg[i] == kNone32 || better(pv, best[i], is_min) ||
-                                    (later && pv == best[i]);
-                  if (take) {
-                    best[i] = pv;
-                    barg[i] = (int32_t)(e_mine - lo);
-                  }
-                }
+                // selects, not branches: lanes disagree on `take` all the time
+                const bool isnan_pv = pv != pv;
+                const bool take =
+                    nanprop ? (barg[i] == kNone32 || isnan_pv || better(pv, best[i], is_min))
+                            : (!isnan_pv && (barg[i] == kNone32 || better(pv, best[i], is_min) ||
+                                             (later && pv == best[i])));
+                best[i] = take ? pv : best[i];
+                barg[i] = take ? (int32_t)(e_mine - lo) : barg[i];
               } else if constexpr (RK == RK_LSE) {
                 float m = (float)best[i];
                 lse_add(m, acc[i], apply_op<float>(x[i], wi, vop));
