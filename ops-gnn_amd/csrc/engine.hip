@@ -37,6 +37,11 @@ Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned) {
     const long v = std::atol(env);
     if (v >= 64) chunk = v / 64 * 64;
   }
+  // Small problems: shrink chunks until there are about 8K wavefronts (8 per
+  // SIMD), so latency is hidden (floor 128 positions: smaller chunks cost
+  // more in row fix-ups than they gain).
+  const int64_t waves_floor = ((nnz_bound / 8192) / 64) * 64;
+  if (!std::getenv("OGN_ENGINE_CHUNK")) chunk = std::min<int64_t>(chunk, std::max<int64_t>(waves_floor, 128));
   pl.chunk = std::min<int64_t>(std::max<int64_t>(chunk, 64), 8192);
   pl.nchunks = std::max<int64_t>(1, (nnz_bound + pl.chunk - 1) / pl.chunk);
   return pl;

@@ -73,17 +73,27 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
   const int64_t total = nrows * ppr;
   const T* __restrict__ src = reinterpret_cast<const T*>(a.src + b * a.src_rows * a.row_bytes);
   T* __restrict__ out = reinterpret_cast<T*>(a.out + (b * a.out_rows + i0) * a.row_bytes);
-  for (int64_t p = threadIdx.x; p < total; p += kThreads) {
-    const int64_t r = fdiv(p, a.ppr);
-    const int64_t q = p - r * ppr;
-    const int64_t s = rows[r];
-    T v;
-    if (s >= 0) {
-      v = src[s * ppr + q];
-    } else {
-      v = T{};
+  // 4 packets per thread per round: all loads issued before the stores
+  constexpr int kU = 4;
+  for (int64_t p0 = threadIdx.x; p0 < total; p0 += kThreads * kU) {
+    T v[kU];
+    int64_t o[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t p = p0 + u * kThreads;
+      o[u] = -1;
+      v[u] = T{};
+      if (p < total) {
+        const int64_t r = fdiv(p, a.ppr);
+        const int64_t q = p - r * ppr;
+        const int64_t s = rows[r];
+        o[u] = r * ppr + q;
+        if (s >= 0) v[u] = src[s * ppr + q];
+      }
     }
-    out[r * ppr + q] = v;
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (o[u] >= 0) out[o[u]] = v[u];
   }
 }
 
