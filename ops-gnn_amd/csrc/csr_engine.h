@@ -317,7 +317,10 @@ void engine_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
       acc[i] = is_prod ? 1.f : 0.f;
-      best[i] = RK == RK_LSE ? (MT)-__builtin_inff() : (MT)0;
+      // min/max start from NaN, "nothing taken yet": every ordered compare
+      // with it is false, so the first non-NaN message is taken without a
+      // separate test (barg stays kNone32 until then)
+      best[i] = RK == RK_LSE ? (MT)-__builtin_inff() : (MT)__builtin_nan("");
       barg[i] = kNone32;
     }
   };
@@ -518,10 +521,17 @@ void engine_kernel(Params p) {
                 const MT pv = apply_op<MT>((MT)x[i], (MT)wi, vop);
                 // selects, not branches: lanes disagree on `take` all the time
                 const bool isnan_pv = pv != pv;
-                const bool take =
-                    nanprop ? (barg[i] == kNone32 || isnan_pv || better(pv, best[i], is_min))
-                            : (!isnan_pv && (barg[i] == kNone32 || better(pv, best[i], is_min) ||
-                                             (later && pv == best[i])));
+                bool take;
+                if constexpr (FAST) {
+                  // NaN-ignoring; `blocked` is false against the NaN start
+                  const bool blocked = VAR == V_LATER ? (is_min ? pv > best[i] : pv < best[i])
+                                                      : (is_min ? pv >= best[i] : pv <= best[i]);
+                  take = !isnan_pv && !blocked;
+                } else {
+                  take = nanprop ? (barg[i] == kNone32 || isnan_pv || better(pv, best[i], is_min))
+                                 : (!isnan_pv && (barg[i] == kNone32 || better(pv, best[i], is_min) ||
+                                                  (later && pv == best[i])));
+                }
                 best[i] = take ? pv : best[i];
                 barg[i] = take ? (int32_t)(e_mine - lo) : barg[i];
               } else if constexpr (RK == RK_LSE) {
