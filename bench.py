@@ -102,6 +102,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (rocprof counter calibration)")
+    ap.add_argument("--torch-compare", action="store_true",
+                    help="also time torch's embedding_bag(sum, per_sample_weights) on the same CSR "
+                         "(a library implementation of the same weighted row gather)")
     ap.add_argument("--workload", choices=["spmm", "segment", "gat", "coo"], default="spmm",
                     help="spmm = config 3 (the headline metric); segment / gat / coo = configs 2 / 4 / 5")
     args = ap.parse_args()
@@ -116,6 +119,7 @@ def main():
         line = {"segment": bench_segment, "gat": bench_gat, "coo": bench_coo}[args.workload](args)
         if args.copy_calibration:
             copy_calibration()
+
         print(json.dumps(line), flush=True)
         return
 
@@ -174,6 +178,28 @@ def main():
         if args.copy_calibration:
             copy_calibration()
 
+        torch_ms = None
+        if args.torch_compare and args.reduce == "sum":
+            offsets = d_ptr[:-1]
+
+            def tstep():
+                return torch.nn.functional.embedding_bag(d_col, d_mat, offsets, mode="sum",
+                                                         per_sample_weights=d_val)
+            ref = tstep()
+            torch.cuda.synchronize()
+            got = step()
+            scale = (got.float() - ref.float()).abs().max().item()
+            log(f"bench: torch embedding_bag max |diff| vs csr_spmm = {scale:.3e}")
+            for _ in range(2):
+                tstep()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                tstep()
+            torch.cuda.synchronize()
+            torch_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+            log(f"bench: torch embedding_bag {torch_ms:.3f} ms per step")
+
     esz = 4 if args.dtype == "f32" else 2
     mm = args.reduce in ("min", "max")
     nbytes = spmm_bytes(m, nnz, k, esz, esz, esz) + (8 * m * k if mm else 0)
@@ -221,6 +247,9 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if torch_ms is not None:
+        result["torch_embedding_bag"] = {"ms_per_step": round(torch_ms, 4),
+                                         "GB/s": round(nbytes / (torch_ms * 1e-3) / 1e9, 2)}
     print(json.dumps(result), flush=True)
 
 
