@@ -239,13 +239,16 @@ enum { V_GENERIC = 0, V_FIRST = 1, V_LATER = 2, V_FIRST32 = 3 };
 // Occupancy target per instance (waves per SIMD), enforced through the
 // register budget: 4 (<= 128 VGPRs) for the fast variants, 3 for 16-bit
 // min/max and log-sum-exp, whose 8 elements per lane need more state.
-template <int DT, int RK, int VAR>
+template <int DT, int RK, int VAR, int G, bool VL>
 constexpr int engine_waves() {
-  return VAR == V_GENERIC ? 1 : (DT != OGN_F32 && RK != RK_SUM ? 3 : 4);
+  if constexpr (VAR == V_GENERIC) return 1;
+  // one 16-byte row per lane: 8 staged positions per lane per window
+  if constexpr (G == 1 && VL) return 3;
+  return DT != OGN_F32 && RK != RK_SUM ? 3 : 4;
 }
 
 template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER, int VAR>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(engine_waves<DT, RK, VAR>())))
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(engine_waves<DT, RK, VAR, G, VL>())))
 void engine_kernel(Params p) {
   using E = Elem<DT>;
   using S_t = typename E::S;
@@ -420,26 +423,43 @@ void engine_kernel(Params p) {
 
   // Column indices and weights of the next 64-position window are loaded
   // one window ahead, so a window's gathers never wait for its staging load.
-  int64_t cl_next = 0;
-  float vl_next = 1.f;
+  // A window is the run of positions whose col / value are staged together:
+  // 64 positions (one per lane) when a step covers fewer than 64 positions,
+  // and kUnroll x 64 when one step already covers 64 (S == 64: one lane per
+  // feature row or one feature), so that kUnroll steps can still be in
+  // flight; each lane then stages its own position of every step.
+  constexpr int WSTEPS = S == kWave ? kUnroll : 1;
+  constexpr int64_t WPOS = (int64_t)kWave * WSTEPS;
+  int64_t cl_next[WSTEPS];
+  float vl_next[WSTEPS];
   auto stage = [&](int64_t wb2) {
-    const int64_t el = wb2 + lane;
-    const bool ev = el < hi;
-    if constexpr (GATHER) cl_next = ev ? (int64_t)load_stream(col + el) : 0;
-    if (val_mode == 1) vl_next = ev ? E::load1(val, el) : 0.f;
+#pragma unroll
+    for (int t = 0; t < WSTEPS; ++t) {
+      const int64_t el = wb2 + t * kWave + lane;
+      const bool ev = el < hi;
+      if constexpr (GATHER) cl_next[t] = ev ? (int64_t)load_stream(col + el) : 0;
+      vl_next[t] = 1.f;
+      if (val_mode == 1) vl_next[t] = ev ? E::load1(val, el) : 0.f;
+    }
   };
   stage(lo);
-  for (int64_t wbase = lo; wbase < hi; wbase += kWave) {
-    int64_t cl;
-    if constexpr (GATHER) {
-      cl = cl_next;
-    } else {
-      cl = wbase + lane;
+  for (int64_t wbase = lo; wbase < hi; wbase += WPOS) {
+    // One-step windows copy the staged col / value out and restage at once;
+    // multi-step windows read the staged arrays in phase 1 and restage after
+    // the gathers are issued (no second copy of the arrays).
+    int64_t cl = 0;
+    float vl = 1.f;
+    if constexpr (WSTEPS == 1) {
+      if constexpr (GATHER) {
+        cl = cl_next[0];
+      } else {
+        cl = wbase + lane;
+      }
+      cl = std::min<int64_t>(std::max<int64_t>(cl, 0), p.n - 1);
+      vl = vl_next[0];
+      if (wbase + WPOS < hi) stage(wbase + WPOS);
     }
-    cl = std::min<int64_t>(std::max<int64_t>(cl, 0), p.n - 1);
-    const float vl = vl_next;
-    if (wbase + kWave < hi) stage(wbase + kWave);
-    const int nw = (int)std::min<int64_t>(kWave, hi - wbase);
+    const int nw = (int)std::min<int64_t>(WPOS, hi - wbase);
     const int nsteps = (nw + S - 1) / S;
     for (int j0 = 0; j0 < nsteps; j0 += kUnroll) {
       // Raw 16-byte loads are kept as issued and unpacked when consumed, so
@@ -457,17 +477,34 @@ void engine_kernel(Params p) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int idx = (j0 + u) * S + sub;
-        if constexpr (GATHER) {
-          if constexpr (OFF32) {
-            co[u] = (uint32_t)shfl32((int32_t)cl, idx & (kWave - 1)) * (uint32_t)(K * sizeof(S_t)) +
-                    (uint32_t)(k0 * sizeof(S_t));
+        if constexpr (WSTEPS > 1) {
+          // S == 64: step u is this lane's own staged position u
+          int64_t c1;
+          if constexpr (GATHER) {
+            c1 = cl_next[u];
           } else {
-            cc[u] = (int64_t)shfl64((IDX)cl, idx & (kWave - 1));
+            c1 = wbase + u * kWave + lane;
           }
+          c1 = std::min<int64_t>(std::max<int64_t>(c1, 0), p.n - 1);
+          if constexpr (GATHER && OFF32) {
+            co[u] = (uint32_t)c1 * (uint32_t)(K * sizeof(S_t)) + (uint32_t)(k0 * sizeof(S_t));
+          } else {
+            cc[u] = c1;
+          }
+          ws[u] = vl_next[u];
         } else {
-          cc[u] = std::min<int64_t>(wbase + idx, p.n - 1);
+          if constexpr (GATHER) {
+            if constexpr (OFF32) {
+              co[u] = (uint32_t)shfl32((int32_t)cl, idx & (kWave - 1)) * (uint32_t)(K * sizeof(S_t)) +
+                      (uint32_t)(k0 * sizeof(S_t));
+            } else {
+              cc[u] = (int64_t)shfl64((IDX)cl, idx & (kWave - 1));
+            }
+          } else {
+            cc[u] = std::min<int64_t>(wbase + idx, p.n - 1);
+          }
+          ws[u] = shflf(vl, idx & (kWave - 1));
         }
-        ws[u] = shflf(vl, idx & (kWave - 1));
       }
       // Phase 2: issue the U gathers back to back.
 #pragma unroll
@@ -495,6 +532,9 @@ void engine_kernel(Params p) {
           w[u][0] = ws[u];
           if (val_mode == 2 && ok) w[u][0] = E::load1(val, (wbase + idx) * K + k0);
         }
+      }
+      if constexpr (WSTEPS > 1) {
+        if (wbase + WPOS < hi) stage(wbase + WPOS);  // every step of this window is issued
       }
       // Phase 3: consume the steps in order (fully unrolled, so the staged
       // steps stay in registers).

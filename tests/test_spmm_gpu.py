@@ -132,6 +132,19 @@ def test_powerlaw_feature_widths(ogn, oracle, k, reduce):
     check_spmm(ogn, oracle, ptr, col, val, mat, reduce, what=f"powerlaw/k{k}/{reduce}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("k", [4, 8, 16])
+@pytest.mark.parametrize("reduce", ["sum", "max"])
+@pytest.mark.parametrize("feature_values", [False, True])
+def test_narrow_rows_16bit(ogn, oracle, dtype, k, reduce, feature_values):
+    # K * 2 bytes <= 32: one or two lanes per row, 64 / 32 positions per step
+    ptr, col, rng = _powerlaw(4000, 3000, 90_000, 9000, seed=10 + k)
+    mat = torch.from_numpy(rng.standard_normal((3000, k), dtype=np.float32)).to(dtype)
+    shape = (col.numel(), k) if feature_values else (col.numel(),)
+    val = torch.from_numpy(rng.random(shape, dtype=np.float32)).to(dtype)
+    check_spmm(ogn, oracle, ptr, col, val, mat, reduce, what=f"narrow/{dtype}/k{k}/{reduce}")
+
+
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("reduce", ["sum", "min", "max"])
 def test_powerlaw_k128_dtypes(ogn, oracle, dtype, reduce):
