@@ -100,9 +100,11 @@ int ogn_validate_csr(const void* rowptr, const void* col, int index_dtype, int64
  *
  *   out[b, r, k] = R_{e in [ptr[r], ptr[r+1])} value[e, (k | 0)] * mat[b, col[e], k]
  *
- * mat: [batch, n, k] of in_dtype (f32/f16/bf16).  value: NULL (all ones), or
- * [nnz] (value_width 1) or [nnz, k] (value_width k), same dtype as mat.
- * out: [batch, m, k] of out_dtype (f32/f16/bf16); arg: [batch, m, k] int64,
+ * mat: [batch, n, k] of in_dtype (f32/f16/bf16, or i8).  value: NULL (all
+ * ones), or [nnz] (value_width 1) or [nnz, k] (value_width k), same dtype as
+ * mat.  out: [batch, m, k] of out_dtype (f32/f16/bf16; i32 for i8 input,
+ * accumulated exactly in int32, mean truncating toward zero, as the
+ * reference's int8 path); arg: [batch, m, k] int64,
  * required for min/max, ignored otherwise.  Arithmetic is fp32 (min/max of
  * fp32 inputs compare exact fp64 products).  min/max ignore NaN products,
  * the first edge wins ties, and an empty or all-NaN row gives 0 / arg = nnz.

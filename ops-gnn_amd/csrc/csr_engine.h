@@ -311,7 +311,10 @@ void engine_kernel(Params p) {
   const bool head_split = rs < lo;
   bool first = true;
 
-  float acc[NE];
+  // int8 sums accumulate exactly in int32 (torch_sparse int8 -> int32)
+  constexpr bool IS_INT = DT == OGN_I8;
+  using AT = std::conditional_t<IS_INT, int32_t, float>;
+  AT acc[NE];
   MT best[NE];
   // Extremum positions are held as int32 offsets from the chunk start (a
   // chunk is at most 8192 positions); kNone32 marks "nothing taken".
@@ -319,7 +322,7 @@ void engine_kernel(Params p) {
   auto reset = [&]() {
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
-      acc[i] = is_prod ? 1.f : 0.f;
+      acc[i] = is_prod ? (AT)1 : (AT)0;
       // min/max start from NaN, "nothing taken yet": every ordered compare
       // with it is false, so the first non-NaN message is taken without a
       // separate test (barg stays kNone32 until then)
@@ -361,8 +364,8 @@ void engine_kernel(Params p) {
         best[i] = m1;
         acc[i] = s1;
       } else {
-        const float o = xor_shfl<off>(acc[i]);
-        const float lo_v = upper ? o : acc[i], hi_v = upper ? acc[i] : o;
+        const AT o = xor_shfl<off>(acc[i]);
+        const AT lo_v = upper ? o : acc[i], hi_v = upper ? acc[i] : o;
         acc[i] = is_prod ? lo_v * hi_v : lo_v + hi_v;
       }
     }
@@ -388,9 +391,9 @@ void engine_kernel(Params p) {
         static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)best[i];
         (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i] == kNone32 ? kNone : lo + barg[i];
       } else if constexpr (RK == RK_LSE) {
-        static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2((float)best[i], acc[i]);
+        static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2((float)best[i], (float)acc[i]);
       } else {
-        static_cast<float*>(head ? p.rec_head : p.rec_tail)[rb + i] = acc[i];
+        static_cast<AT*>(head ? p.rec_head : p.rec_tail)[rb + i] = acc[i];
       }
     }
   };
@@ -402,13 +405,24 @@ void engine_kernel(Params p) {
     } else if (sub == 0 && kok) {
       float v[NE];
       int64_t ag[NE];
-#pragma unroll
-      for (int i = 0; i < NE; ++i)
-        finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, acc[i], best[i],
-                            barg[i] == kNone32 ? kNone : lo + barg[i], &v[i], &ag[i]);
       const int64_t off = b * p.out_bstride + r * K + k0;
-      if (VL || k0 + NE <= K) {
-        store_floats<NE, true>(p.out, p.out_dt, off, v);
+      if constexpr (IS_INT && RK == RK_SUM) {
+        // integer sum / mean (mean truncates toward zero), int32 output
+        const int32_t cnt = (int32_t)(re - rs);
+        int32_t* o = static_cast<int32_t*>(p.out) + off;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+          if (!VL && k0 + i >= K) break;
+          o[i] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? acc[i] / cnt : 0) : acc[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+          finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, (float)acc[i], best[i],
+                              barg[i] == kNone32 ? kNone : lo + barg[i], &v[i], &ag[i]);
+        if (VL || k0 + NE <= K) {
+          store_floats<NE, true>(p.out, p.out_dt, off, v);
+        }
       }
       if constexpr (RK == RK_MINMAX) {
         if (p.arg) {
@@ -578,6 +592,8 @@ void engine_kernel(Params p) {
                 float m = (float)best[i];
                 lse_add(m, acc[i], apply_op<float>(x[i], wi, vop));
                 best[i] = m;
+              } else if constexpr (IS_INT) {
+                acc[i] += (int32_t)(x[i] * wi);  // exact: |x w| <= 2^14
               } else {
                 if (vop == OP_MUL)
                   acc[i] = is_prod ? acc[i] * (x[i] * wi) : __builtin_fmaf(x[i], wi, acc[i]);
@@ -613,9 +629,11 @@ void engine_kernel(Params p) {
 // Finish rows that cross chunk boundaries: one wave per chunk that holds the
 // first piece of such a row; loads of the partial records are issued in
 // groups of 8 and folded in chunk order.
-template <typename IDX, int RK, bool F32MM>
+// INT: int32 sum records and an int32 output (int8 SpMM).
+template <typename IDX, int RK, bool F32MM, bool INT = false>
 __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   using MT = std::conditional_t<F32MM, double, float>;
+  using AT = std::conditional_t<INT, int32_t, float>;
   const int lane = lane_id();
   const int64_t c = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   const int64_t b = blockIdx.z;
@@ -639,7 +657,7 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   constexpr int kBatch = 8;
   for (int64_t k = lane; k < K; k += kWave) {
     const int64_t base_rec = (b * p.nchunks) * K + k;
-    float a = 0.f;
+    AT a = 0;
     MT best = 0;
     int64_t barg = kNone;
     if constexpr (RK == RK_MINMAX) {
@@ -650,10 +668,11 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
       best = t.x;
       a = t.y;
     } else {
-      a = static_cast<const float*>(p.rec_tail)[base_rec + c * K];
+      a = static_cast<const AT*>(p.rec_tail)[base_rec + c * K];
     }
     for (int64_t c0 = c + 1; c0 <= c2; c0 += kBatch) {
-      float va[kBatch], vb[kBatch];
+      AT va[kBatch];
+      float vb[kBatch];
       double vd[kBatch];
       int64_t vg[kBatch];
 #pragma unroll
@@ -671,7 +690,7 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
           va[j] = t.x;
           vb[j] = t.y;
         } else {
-          va[j] = ok ? static_cast<const float*>(head ? p.rec_head : p.rec_tail)[ri] : (is_prod ? 1.f : 0.f);
+          va[j] = ok ? static_cast<const AT*>(head ? p.rec_head : p.rec_tail)[ri] : (is_prod ? (AT)1 : (AT)0);
         }
       }
 #pragma unroll
@@ -687,17 +706,24 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
           }
         } else if constexpr (RK == RK_LSE) {
           float m = (float)best;
-          lse_merge(m, a, va[j], vb[j]);
+          float sa = (float)a;
+          lse_merge(m, sa, (float)va[j], vb[j]);
           best = m;
+          a = (AT)sa;
         } else {
           a = is_prod ? a * va[j] : a + va[j];
         }
       }
     }
+    const int64_t off = b * p.out_bstride + r * K + k;
+    if constexpr (INT && RK == RK_SUM) {
+      const int32_t cnt = (int32_t)(re - rs);
+      static_cast<int32_t*>(p.out)[off] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? a / cnt : 0) : a;
+      continue;
+    }
     float v;
     int64_t ag = 0;
-    finish_elem<RK, MT>(p, b, r, k, rs, re, a, best, barg, &v, &ag);
-    const int64_t off = b * p.out_bstride + r * K + k;
+    finish_elem<RK, MT>(p, b, r, k, rs, re, (float)a, best, barg, &v, &ag);
     store_floats<1>(p.out, p.out_dt, off, &v);
     if constexpr (RK == RK_MINMAX) {
       if (p.arg) p.arg[off] = ag;
@@ -736,6 +762,7 @@ OGN_ENGINE_DECL(launch_gather_bf16)
 OGN_ENGINE_DECL(launch_contig_f32)
 OGN_ENGINE_DECL(launch_contig_f16)
 OGN_ENGINE_DECL(launch_contig_bf16)
+OGN_ENGINE_DECL(launch_gather_i8)
 #undef OGN_ENGINE_DECL
 
 template <int DT, typename IDX, bool VL, int RK, bool GATHER, int VAR>

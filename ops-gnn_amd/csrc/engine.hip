@@ -100,6 +100,9 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
       case OGN_F16:
         gather ? launch_gather_f16(pl, rk, i64, grid, s, p) : launch_contig_f16(pl, rk, i64, grid, s, p);
         break;
+      case OGN_I8:
+        launch_gather_i8(pl, rk, i64, grid, s, p);  // gather mode only (torch_sparse int8 SpMM)
+        break;
       default:
         gather ? launch_gather_bf16(pl, rk, i64, grid, s, p) : launch_contig_bf16(pl, rk, i64, grid, s, p);
         break;
@@ -118,7 +121,10 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
     case RK_LSE: hipLaunchKernelGGL((fixup_kernel<IDX, RK_LSE, false>), fg, dim3(kBlock), 0, s, p); break; \
     default: hipLaunchKernelGGL((fixup_kernel<IDX, RK_SUM, false>), fg, dim3(kBlock), 0, s, p); break;     \
   }
-    if (i64) {
+    if (in_dtype == OGN_I8 && rk == RK_SUM) {
+      if (i64) hipLaunchKernelGGL((fixup_kernel<int64_t, RK_SUM, false, true>), fg, dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL((fixup_kernel<int32_t, RK_SUM, false, true>), fg, dim3(kBlock), 0, s, p);
+    } else if (i64) {
       OGN_FIX(int64_t)
     } else {
       OGN_FIX(int32_t)

@@ -150,6 +150,24 @@ template <> struct Elem<OGN_BF16> {
   }
 };
 
+// int8 features (torch_sparse SpMM int8 -> int32): values widen to float
+// exactly; products of two int8 values (|x w| <= 2^14) are exact in fp32.
+template <> struct Elem<OGN_I8> {
+  using S = int8_t;
+  static constexpr int VEC = 16;
+  __device__ static __forceinline__ float load1(const void* p, int64_t i) {
+    return (float)static_cast<const int8_t*>(p)[i];
+  }
+  __device__ static __forceinline__ void unpack(const uint4& v, float* x) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * i + j] = (float)(int8_t)((w[i] >> (8 * j)) & 0xffu);
+    }
+  }
+};
+
 __host__ __device__ constexpr int dtype_size(int dt) {
   return dt == OGN_F32 || dt == OGN_I32 ? 4
        : dt == OGN_I64 || dt == OGN_F64 ? 8
@@ -163,6 +181,12 @@ __host__ __device__ constexpr int dtype_size(int dt) {
 template <int N, bool NT = false>
 __device__ __forceinline__ void store_floats(void* out, int dt, int64_t off,
                                              const float* v) {
+  if (dt == OGN_I32) {
+    int32_t* p = static_cast<int32_t*>(out) + off;
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = (int32_t)v[i];
+    return;
+  }
   if (dt == OGN_F32) {
     float* p = static_cast<float*>(out) + off;
     if constexpr (N % 4 == 0) {

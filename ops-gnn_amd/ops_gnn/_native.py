@@ -16,8 +16,10 @@ import torch
 from . import _lib
 from ._lib import check, dptr, lib, stream_of
 
-SPMM_INPUT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
-SPMM_OUTPUT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+SPMM_INPUT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.int8)
+SPMM_OUTPUT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.int32)
+# int8 mat / value give an int32 result (reference python/ops_gnn/torch_sparse_spmm.py:213)
+SPMM_FLOAT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 
 
 def _index_code(t: torch.Tensor) -> int:
@@ -58,9 +60,9 @@ def spmm_forward(ptr: torch.Tensor, col: torch.Tensor, value: Optional[torch.Ten
     empty int64 tensor).
     """
     if mat.dtype not in SPMM_INPUT_DTYPES:
-        raise ValueError("mat must be float32, float16 or bfloat16")
-    if out_dtype not in SPMM_OUTPUT_DTYPES:
-        raise ValueError("unsupported output dtype")
+        raise ValueError("mat must be float32, float16, bfloat16 or int8")
+    if out_dtype not in SPMM_OUTPUT_DTYPES or ((mat.dtype == torch.int8) != (out_dtype == torch.int32)):
+        raise ValueError("unsupported output dtype (int8 input gives int32, float inputs a float dtype)")
     mat = mat.contiguous()
     ptr = ptr.contiguous()
     col = col.contiguous()

@@ -38,7 +38,7 @@ _INPUT_DTYPES = _native.SPMM_INPUT_DTYPES
 def _check_mat(mat):
     """reference python/ops_gnn/torch_sparse_spmm.py:35-37."""
     if mat.device.type != "cuda" or mat.dim() < 2 or mat.dtype not in _INPUT_DTYPES:
-        raise ValueError("mat must be a GPU fp32/fp16/bf16 tensor [...,N,K]")
+        raise ValueError("mat must be a GPU fp32/fp16/bf16/int8 tensor [...,N,K]")
 
 
 def _check_value(value, edges, mat):
@@ -221,8 +221,8 @@ def _dispatch(ptr, col, value, mat, reduce, *, row=None, rowcount=None, colptr=N
     _validate(ptr, col, mat.size(-2))
     if reduce < 2:
         _grad_meta(ptr, col, value, mat, reduce, row=row, rowcount=rowcount, colptr=colptr, perm=perm)
-    dtype = output_dtype or mat.dtype
-    if dtype not in _native.SPMM_OUTPUT_DTYPES:
+    dtype = output_dtype or (torch.int32 if mat.dtype == torch.int8 else mat.dtype)
+    if dtype not in _native.SPMM_OUTPUT_DTYPES or ((mat.dtype == torch.int8) != (dtype == torch.int32)):
         raise ValueError("unsupported output dtype")
     if not torch.is_grad_enabled() or not (mat.requires_grad or (value is not None and value.requires_grad)):
         return _native.spmm_forward(ptr, col, value, mat, reduce, dtype)

@@ -145,6 +145,35 @@ def test_narrow_rows_16bit(ogn, oracle, dtype, k, reduce, feature_values):
     check_spmm(ogn, oracle, ptr, col, val, mat, reduce, what=f"narrow/{dtype}/k{k}/{reduce}")
 
 
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("k,feature_values", [(16, False), (128, False), (32, True), (5, False)])
+def test_int8_to_int32(ogn, oracle, reduce, k, feature_values):
+    # reference golden test/torch_sparse_spmm/arch35/golden.py:91-116: int8
+    # mat / value, fp64 arithmetic, trunc, int32 output; first-tie args
+    ptr, col, rng = _powerlaw(3000, 2000, 70_000, 9000, seed=20 + k)
+    mat = torch.from_numpy(rng.integers(-128, 128, (2000, k)).astype(np.int8))
+    shape = (col.numel(), k) if feature_values else (col.numel(),)
+    val = torch.from_numpy(rng.integers(-128, 128, shape).astype(np.int8))
+    res = ogn.csr_spmm(ptr.cuda(), col.cuda(), val.cuda(), mat.cuda(), reduce)
+    got, arg = res if reduce in ("min", "max") else (res, None)
+    assert got.dtype == torch.int32
+    gold, garg = oracle.spmm_csr(ptr, col, val.float(), mat.float(), reduce)
+    want = np.trunc(gold).astype(np.int32)
+    assert_exact(got, want, f"int8/{reduce}/k{k} values")
+    if arg is not None:
+        assert_exact(arg, garg, f"int8/{reduce}/k{k} arg")
+
+
+def test_int8_output_dtype_contract(ogn):
+    ptr = torch.tensor([0, 1, 2], device="cuda")
+    col = torch.tensor([0, 1], device="cuda")
+    mat = torch.ones((2, 4), dtype=torch.int8, device="cuda")
+    with pytest.raises(ValueError, match="output dtype"):
+        ogn.csr_spmm(ptr, col, None, mat, "sum", output_dtype=torch.float32)
+    with pytest.raises(ValueError, match="output dtype"):
+        ogn.csr_spmm(ptr, col, None, mat.float(), "sum", output_dtype=torch.int32)
+
+
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("reduce", ["sum", "min", "max"])
 def test_powerlaw_k128_dtypes(ogn, oracle, dtype, reduce):
