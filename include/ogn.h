@@ -44,7 +44,8 @@ typedef enum {
   OGN_I32 = 4,
   OGN_I64 = 5,
   OGN_F64 = 6,
-  OGN_U8 = 7
+  OGN_U8 = 7,
+  OGN_I16 = 8
 } ogn_dtype;
 
 typedef enum {
@@ -179,7 +180,14 @@ int ogn_ptr2ind(const void* ptr, int index_dtype, int64_t rows, int64_t numel, i
  * indptr: int64 [ptr_batches, segments + 1], ptr_batches 1 (shared by every
  * batch) or `batch`; non-decreasing, within [0, length].  Segment s covers
  * rows [indptr[s], indptr[s+1]); rows outside [indptr[0], indptr[segments])
- * are ignored.  dtype: f32 / f16 / bf16 for src and out; arithmetic in fp32.
+ * are ignored.  dtype: f32 / f16 / bf16 for src and out, arithmetic in fp32;
+ * or an exact dtype (int8, uint8, int16, int32, int64, float64): sums and
+ * products wrap in the dtype, min/max compare exactly, and the integer mean
+ * follows each operator's rule (segment_csr: narrow(sum) / narrow(count)
+ * truncating, 0 for a zero narrowed count; segment_coo: the same with the
+ * exact mean for a zero narrowed count; scatter: floor division by the count,
+ * narrowed and clamped to >= 1 for 8/16-bit types).  Exact dtypes need no
+ * workspace and support sum, mean, min, max (and prod for scatter).
  * reduce: sum, mean, min, max, prod, lse.  arg (int64, optional, min/max
  * only) gets positions along the reduction dim.
  *
@@ -249,8 +257,10 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
  * (strides in elements, 0 = broadcast); out/arg: [before, size, after]; when
  * has_out, out holds the starting values.  reduce: sum, mean, min, max,
  * prod.  arg (int64) is required for min/max.  Entries of index outside
- * [0, size) are skipped.  fp32 atomics: sum/mean/prod order may vary between
- * runs; min/max and arg are exact.  Replaces scatter_forward
+ * [0, size) are skipped.  dtype: f32 / f16 / bf16 (fp32 atomics: sum/mean/prod
+ * order may vary between runs; min/max and arg are exact), int8 / uint8 /
+ * int16 / int32 / int64 (64-bit integer atomics: every result exact and
+ * order-independent) or float64 (sum/prod order may vary).  Replaces scatter_forward
  * (reference csrc/npu/scatter/op_host/scatter.cpp:242-269) and its atomic and
  * min/max kernels (csrc/npu/scatter/op_kernel/arch35/scatter_kernel_atomic.h:338-412,
  * scatter_kernel_minmax.h:120-175). */

@@ -55,7 +55,16 @@ def _compile(src: Path, obj: Path) -> None:
         sys.stderr.write("\n".join(noise) + "\n")
 
 
-def build(jobs: int = 8, verbose: bool = True) -> Path:
+def _stale(src: Path, obj: Path, headers) -> bool:
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    return src.stat().st_mtime > t or any(h.stat().st_mtime > t for h in headers)
+
+
+def build(jobs: int = 8, verbose: bool = True, incremental: bool = False) -> Path:
+    """Compile every source (or, with incremental, those whose object is older
+    than the source or any header) and link the library."""
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
@@ -63,7 +72,9 @@ def build(jobs: int = 8, verbose: bool = True) -> Path:
     obj_dir.mkdir(exist_ok=True)
     objs = [obj_dir / (s.stem + ".o") for s in sources]
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        futures = [pool.submit(_compile, s, o) for s, o in zip(sources, objs)]
+        headers = list(CSRC.glob("*.h")) + [HERE.parent / "include" / "ogn.h"]
+        futures = [pool.submit(_compile, s, o) for s, o in zip(sources, objs)
+                   if not incremental or _stale(s, o, headers)]
         for f in futures:
             f.result()
     target = OUT_DIR / LIB_NAME
@@ -81,5 +92,6 @@ def build(jobs: int = 8, verbose: bool = True) -> Path:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", "--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--incremental", action="store_true", help="recompile only out-of-date objects")
     args = ap.parse_args()
-    build(args.jobs)
+    build(args.jobs, incremental=args.incremental)

@@ -14,6 +14,7 @@
 // sorted, from atomics otherwise -- then one elementwise pass produces
 // softmax / log_softmax, or one pass over the groups produces logsumexp.
 #include "ogn_device.h"
+#include "typed.h"
 
 #include <algorithm>
 #include <string>
@@ -443,7 +444,9 @@ extern "C" {
 
 size_t ogn_scatter_atomic_workspace_size(int64_t before, int64_t size, int64_t after, int reduce) {
   const size_t cells = (size_t)std::max<int64_t>(before, 0) * std::max<int64_t>(size, 0) * std::max<int64_t>(after, 0);
-  return align256(cells * 4) + (reduce == OGN_REDUCE_MEAN ? align256(cells * 4) : 0) + 256;
+  // sized for the widest accumulator (8 bytes: integer and float64 dtypes)
+  return std::max(align256(cells * 4) + (reduce == OGN_REDUCE_MEAN ? align256(cells * 4) : 0) + 256,
+                  exact_scatter_workspace_size((int64_t)cells, reduce));
 }
 
 int ogn_scatter_atomic(const void* src, int dtype, const int64_t* index, int64_t index_stride_before,
@@ -451,8 +454,9 @@ int ogn_scatter_atomic(const void* src, int dtype, const int64_t* index, int64_t
                        int64_t after, int64_t size, void* out, int64_t* arg, int reduce, int has_out,
                        void* workspace, size_t workspace_bytes, void* stream) {
   if (before < 0 || len < 0 || after < 0 || size < 0) return fail(OGN_EINVAL, "ogn_scatter_atomic: negative size");
-  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
-    return fail(OGN_EUNSUPPORTED, "ogn_scatter_atomic: dtype must be float32, float16 or bfloat16");
+  const bool exact = is_exact_dtype(dtype);
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16 && !exact)
+    return fail(OGN_EUNSUPPORTED, "ogn_scatter_atomic: unsupported dtype");
   if (reduce < OGN_REDUCE_SUM || reduce > OGN_REDUCE_PROD)
     return fail(OGN_EINVAL, "ogn_scatter_atomic: reduce must be sum/mean/min/max/prod");
   const int64_t cells = before * size * after;
@@ -463,6 +467,9 @@ int ogn_scatter_atomic(const void* src, int dtype, const int64_t* index, int64_t
   if (!workspace || workspace_bytes < ogn_scatter_atomic_workspace_size(before, size, after, reduce))
     return fail(OGN_EINVAL, "ogn_scatter_atomic: workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (exact)
+    return exact_scatter_atomic(src, dtype, index, index_stride_before, index_stride_len, index_stride_after, before,
+                                len, after, size, out, arg, reduce, has_out, workspace, s);
   ScatterArgs a{};
   a.src = src;
   a.dt = dtype;

@@ -2,6 +2,7 @@
 // sorted-index scatter, segment_logsumexp): the CSR engine in contiguous mode,
 // plus the index helpers those paths need (batched ind2ptr, index facts).
 #include "csr_engine.h"
+#include "typed.h"
 
 #include <string>
 
@@ -71,7 +72,7 @@ extern "C" {
 
 size_t ogn_segment_reduce_workspace_size(int64_t batch, int64_t length, int64_t segments, int64_t k,
                                          int64_t ptr_batches, int in_dtype, int reduce) {
-  if (batch <= 0 || length < 0 || segments < 0 || k <= 0) return 0;
+  if (batch <= 0 || length < 0 || segments < 0 || k <= 0 || is_exact_dtype(in_dtype)) return 0;
   const int rk = rk_of(reduce);
   const Plan pa = make_plan(length, k, in_dtype, true);
   const Plan pu = make_plan(length, k, in_dtype, false);
@@ -85,8 +86,9 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
                        size_t workspace_bytes, void* stream) {
   if (batch < 0 || length < 0 || segments < 0 || k < 0)
     return fail(OGN_EINVAL, "ogn_segment_reduce: negative size");
-  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
-    return fail(OGN_EUNSUPPORTED, "ogn_segment_reduce: src dtype must be float32, float16 or bfloat16");
+  const bool exact = is_exact_dtype(dtype);
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16 && !exact)
+    return fail(OGN_EUNSUPPORTED, "ogn_segment_reduce: unsupported src dtype");
   if (reduce < OGN_REDUCE_SUM || reduce > OGN_REDUCE_LSE)
     return fail(OGN_EINVAL, "ogn_segment_reduce: unknown reduce code");
   if (semantics < OGN_SEM_SEGMENT_CSR || semantics > OGN_SEM_DGL)
@@ -98,6 +100,9 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
   if (!indptr || !out) return fail(OGN_EINVAL, "ogn_segment_reduce: null pointer");
   if (length > 0 && !src) return fail(OGN_EINVAL, "ogn_segment_reduce: null src");
   const bool has_out = (flags & OGN_SEG_HAS_OUT) != 0;
+  if (exact)
+    return exact_segment_reduce(indptr, ptr_batches, src, dtype, batch, length, segments, k, out, arg, reduce,
+                                semantics, has_out ? 1 : 0, static_cast<hipStream_t>(stream));
 
   const bool aligned = is_aligned(src, 16) && is_aligned(out, 16);
   const Plan pl = make_plan(length, k, dtype, aligned);

@@ -26,7 +26,7 @@ except OSError as exc:  # pragma: no cover - exercised only on a broken install
 arch = "gfx950"
 
 # dtype codes (include/ogn.h ogn_dtype)
-F32, F16, BF16, I8, I32, I64, F64, U8 = range(8)
+F32, F16, BF16, I8, I32, I64, F64, U8, I16 = range(9)
 TORCH_TO_OGN = {
     torch.float32: F32,
     torch.float16: F16,
@@ -36,6 +36,7 @@ TORCH_TO_OGN = {
     torch.int64: I64,
     torch.float64: F64,
     torch.uint8: U8,
+    torch.int16: I16,
 }
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3

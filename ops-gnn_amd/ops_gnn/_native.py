@@ -96,6 +96,11 @@ def spmm_forward(ptr: torch.Tensor, col: torch.Tensor, value: Optional[torch.Ten
 
 # ------------------------------------------------------------------ segment engine
 SEGMENT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+# exact-arithmetic dtypes of segment_csr / segment_coo (reference
+# test/segment_csr/arch35/test_segment_csr.py SUPPORTED_DTYPES) and of scatter
+# (test/scatter/arch35/test_scatter.py DTYPES)
+SEGMENT_EXACT_DTYPES = (torch.int8, torch.uint8, torch.int32, torch.int64)
+SCATTER_DTYPES = SEGMENT_DTYPES + (torch.float64, torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8)
 
 
 def segment_reduce(src3: torch.Tensor, ptr2d: torch.Tensor, segments: int, reduce: int, semantics: int,

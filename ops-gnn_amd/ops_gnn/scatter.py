@@ -13,7 +13,10 @@ Two execution paths, both HIP:
     with OGN_SEM_SCATTER);
   * any other index -> the atomic scatter (ogn_scatter_atomic).
 Index sortedness and bounds come from one cached device probe per index
-version.  float32 / float16 / bfloat16 only; other dtypes raise TypeError.
+version.  float32 / float16 / bfloat16 (fp32 arithmetic), float64, and
+int8 / uint8 / int16 / int32 / int64 (exact, wrapping in the dtype; the mean
+floors, with 8/16-bit counts narrowed as torch_scatter does, reference
+python/ops_gnn/scatter.py:430-458); other dtypes raise TypeError.
 """
 
 import math
@@ -22,7 +25,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib, _native
-from ._native import SEGMENT_DTYPES
+from ._native import SCATTER_DTYPES
 
 _REDUCE_CODE = {"sum": _lib.R_SUM, "add": _lib.R_SUM, "mul": _lib.R_PROD, "mean": _lib.R_MEAN,
                 "min": _lib.R_MIN, "max": _lib.R_MAX}
@@ -44,6 +47,13 @@ def broadcast(src: torch.Tensor, other: torch.Tensor, dim: int) -> torch.Tensor:
     return src.expand(other.size())
 
 
+def _index_extent(index: torch.Tensor, dim: int) -> int:
+    """Size of `index` along `dim` once `broadcast` has placed its dims."""
+    if index.dim() == 1:
+        return index.numel()
+    return index.size(dim) if index.dim() > dim else 1
+
+
 def _normalize_dim(src: torch.Tensor, dim: int) -> int:
     if not isinstance(dim, int) or isinstance(dim, bool):
         raise TypeError("dim must be an int")
@@ -62,9 +72,15 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
     dim = _normalize_dim(src, dim)
     if index.dtype != torch.int64:
         raise TypeError(f"index must have dtype torch.int64, got {index.dtype}")
-    if src.dtype not in SEGMENT_DTYPES:
-        raise TypeError(f"scatter: unsupported dtype {src.dtype} (float32, float16 and bfloat16 run on the GPU)")
+    if src.dtype not in SCATTER_DTYPES:
+        raise TypeError(f"scatter: unsupported dtype {src.dtype}")
     _lib.require_gpu(src, index, what="scatter")
+    if reduce == "mean" and src.size(dim) > 1 and _index_extent(index, dim) == 1:
+        # torch_scatter counts the mean's denominators over the index's own
+        # shape (reference python/ops_gnn/scatter.py:437-449): an index of
+        # extent 1 along dim, broadcast over it, counts each target once, so
+        # the mean of such a scatter is its sum.
+        reduce = "sum"
     expanded = broadcast(index, src, dim)
     compact = index.dim() == 1 and index.numel() == src.size(dim)
     line = index

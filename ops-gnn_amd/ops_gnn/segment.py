@@ -5,9 +5,11 @@ Public names, signatures and return conventions follow the reference
 segment_coo.py:33-128, segment_logsumexp.py:108-155,
 segment_max_csr.py:19-50).  Every reduction runs on the contiguous-segment
 CSR engine (include/ogn.h ogn_segment_reduce): deterministic, one writer per
-output, nnz-balanced across wavefronts.  Supported dtypes: float32, float16,
-bfloat16 (fp32 arithmetic); other dtypes raise TypeError -- there is no CPU
-fallback.
+output, nnz-balanced across wavefronts.  segment_csr / segment_coo take
+float32, float16, bfloat16 (fp32 arithmetic) and int8, uint8, int32, int64
+(exact integer arithmetic wrapping in the dtype, on the exact-dtype segment
+kernel); segment_logsumexp takes the floating dtypes.  Other dtypes raise
+TypeError -- there is no CPU fallback.
 """
 
 import math
@@ -16,7 +18,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib, _native
-from ._native import SEGMENT_DTYPES
+from ._native import SEGMENT_DTYPES, SEGMENT_EXACT_DTYPES
 
 _REDUCE_OPS = ("sum", "add", "mean", "min", "max")
 _CODE = {"sum": _lib.R_SUM, "add": _lib.R_SUM, "mean": _lib.R_MEAN, "min": _lib.R_MIN, "max": _lib.R_MAX}
@@ -31,8 +33,9 @@ def _check_reduce(reduce: str) -> None:
 
 
 def _check_dtype(src: torch.Tensor, op: str) -> None:
-    if src.dtype not in SEGMENT_DTYPES:
-        raise TypeError(f"{op}: unsupported dtype {src.dtype} (float32, float16 and bfloat16 run on the GPU)")
+    if src.dtype not in SEGMENT_DTYPES + SEGMENT_EXACT_DTYPES:
+        raise TypeError(f"{op}: unsupported dtype {src.dtype} (float32, float16, bfloat16, int8, uint8, int32 "
+                        f"and int64 run on the GPU)")
 
 
 def _split(shape, dim):

@@ -218,8 +218,9 @@ void oracle_segment_coo(const float* src, const int64_t* index, int64_t ib, int6
  * (min/max), and positions never taken by min/max become 0.  arg = len when
  * nothing was taken.  reduce codes: 0 sum 1 mean 2 min 3 max 4 prod.
  */
-void oracle_scatter(const float* src, const int64_t* index, int64_t before, int64_t len, int64_t after,
-                    int64_t size, int reduce, int has_out, double limit, double* out, int64_t* arg) {
+static void scatter_fold(const float* src32, const double* src64, const int64_t* index, int64_t before,
+                         int64_t len, int64_t after, int64_t size, int reduce, int has_out, double limit,
+                         double* out, int64_t* arg) {
   const int64_t total = before * size * after;
   int64_t* count = 0;
   if (reduce == 1) {
@@ -234,7 +235,8 @@ void oracle_scatter(const float* src, const int64_t* index, int64_t before, int6
       for (int64_t f = 0; f < after; ++f) {
         const int64_t t = index[(b * len + l) * after + f];
         if (t < 0 || t >= size) continue;
-        const double x = (double)src[(b * len + l) * after + f];
+        const int64_t e = (b * len + l) * after + f;
+        const double x = src32 ? (double)src32[e] : src64[e];
         const int64_t key = (b * size + t) * after + f;
         if (reduce == 0 || reduce == 1) {
           out[key] += x;
@@ -255,6 +257,18 @@ void oracle_scatter(const float* src, const int64_t* index, int64_t before, int6
     for (int64_t i = 0; i < total; ++i)
       if (arg[i] == len) out[i] = 0.0;
   }
+}
+
+void oracle_scatter(const float* src, const int64_t* index, int64_t before, int64_t len, int64_t after,
+                    int64_t size, int reduce, int has_out, double limit, double* out, int64_t* arg) {
+  scatter_fold(src, 0, index, before, len, after, size, reduce, has_out, limit, out, arg);
+}
+
+/* float64 scatter: the same fold on double inputs (the golden computes in
+ * the source dtype, float64 here, in element order). */
+void oracle_scatter_f64(const double* src, const int64_t* index, int64_t before, int64_t len, int64_t after,
+                        int64_t size, int reduce, int has_out, double* out, int64_t* arg) {
+  scatter_fold(0, src, index, before, len, after, size, reduce, has_out, 1.7976931348623157e308, out, arg);
 }
 
 /* ---------------------------------------------------------------- log-sum-exp
@@ -513,4 +527,187 @@ void oracle_gather_coo(const int64_t* index, const unsigned char* src, int64_t b
     for (int64_t e = 0; e < entries; ++e)
       memcpy(out + (b * entries + e) * row_bytes, src + (b * src_rows + index[b * entries + e]) * row_bytes,
              (size_t)row_bytes);
+}
+
+/* ---------------------------------------------------------------- exact integer dtypes
+ * Integer segment_csr / segment_coo / scatter.  Values travel as int64 (any
+ * int8 / uint8 / int16 / int32 / int64 input widens exactly); `bits` and
+ * `is_unsigned` name the source dtype, and narrow() gives the value of that
+ * dtype an int64 wraps to -- the golden's `.to(dtype)`.  Every fold runs in
+ * element order and wraps in the dtype at each step (uint64 arithmetic, then
+ * narrow), exactly as the goldens' typed tensors do.
+ */
+static int64_t narrow(int64_t v, int bits, int is_unsigned) {
+  if (bits >= 64) return v;
+  const uint64_t m = (1ull << bits) - 1;
+  const uint64_t u = (uint64_t)v & m;
+  if (!is_unsigned && (u >> (bits - 1))) return (int64_t)(u | ~m);
+  return (int64_t)u;
+}
+
+static int64_t trunc_div(int64_t a, int64_t b) { return a / b; } /* C division truncates */
+
+static int64_t floor_div(int64_t a, int64_t b) {
+  const int64_t q = a / b;
+  return (a % b != 0 && ((a < 0) != (b < 0))) ? q - 1 : q;
+}
+
+static int64_t int_limit(int bits, int is_unsigned, int want_max) {
+  if (is_unsigned) return want_max ? (int64_t)((1ull << bits) - 1) : 0;
+  if (bits >= 64) return want_max ? INT64_MAX : INT64_MIN;
+  return want_max ? (int64_t)((1ull << (bits - 1)) - 1) : -(int64_t)(1ull << (bits - 1));
+}
+
+/* segment_csr, reference test/segment_csr/arch35/golden.py:21-103: per
+ * segment, sum = typed sum (`selected.sum(0).to(dtype)`); mean =
+ * _mean_from_typed_sum (golden :21-34): count narrowed to the dtype, truncating
+ * division, 0 where the narrowed count is 0; min/max = torch.min/max over the
+ * rows, first extremum for arg (segment_argminmax_cpu, golden :84-103).
+ * Empty segments: 0, arg = len.  End pointers clamp to len (golden :64). */
+void oracle_int_segment_csr(const int64_t* src, const int64_t* ptr, int64_t ptr_stride, int64_t batch,
+                            int64_t len, int64_t feat, int64_t segs, int reduce, int bits, int is_unsigned,
+                            int64_t* out, int64_t* arg) {
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t* p = ptr + b * ptr_stride;
+    for (int64_t s = 0; s < segs; ++s) {
+      int64_t a = p[s], z = p[s + 1];
+      if (z > len) z = len;
+      for (int64_t j = 0; j < feat; ++j) {
+        const int64_t o = (b * segs + s) * feat + j;
+        if (arg) arg[o] = len;
+        if (a >= z) {
+          out[o] = 0;
+          continue;
+        }
+        if (reduce <= 1) {
+          int64_t acc = 0;
+          for (int64_t i = a; i < z; ++i) acc = narrow((int64_t)((uint64_t)acc + (uint64_t)src[(b * len + i) * feat + j]), bits, is_unsigned);
+          if (reduce == 1) {
+            const int64_t c = narrow(z - a, bits, is_unsigned);
+            acc = c == 0 ? 0 : narrow(trunc_div(acc, c), bits, is_unsigned);
+          }
+          out[o] = acc;
+        } else {
+          int64_t best = src[(b * len + a) * feat + j], where = a;
+          for (int64_t i = a + 1; i < z; ++i) {
+            const int64_t v = src[(b * len + i) * feat + j];
+            if (reduce == 2 ? v < best : v > best) {
+              best = v;
+              where = i;
+            }
+          }
+          out[o] = best;
+          if (arg) arg[o] = where;
+        }
+      }
+    }
+  }
+}
+
+/* segment_coo, reference csrc/npu/segment_coo/op_kernel/arch35/segment_coo.cpp:114-153
+ * (ReduceSegments) with FinishMean (:18-31), as an in-order fold over the
+ * sorted index (same layout and seeding rules as oracle_segment_coo above).
+ * mean: sum from out (has_out) or 0; a non-empty segment gives
+ * narrow(narrow(sum) / narrow(count)), or the exact sum / count when the
+ * narrowed count is 0 (a byte count divisible by 256). */
+void oracle_int_segment_coo(const int64_t* src, const int64_t* index, int64_t ib, int64_t batch, int64_t len,
+                            int64_t feat, int64_t segs, int reduce, int has_out, int bits, int is_unsigned,
+                            int64_t* out, int64_t* arg) {
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t* idx = index + (ib == 1 ? 0 : b * len);
+    int64_t* o = out + b * segs * feat;
+    int64_t* ag = arg ? arg + b * segs * feat : 0;
+    for (int64_t i = 0; i < segs * feat; ++i) {
+      if (reduce == 0 || !has_out) o[i] = 0;
+      if (ag) ag[i] = len;
+    }
+    int64_t j = 0;
+    while (j < len) {
+      const int64_t s = idx[j];
+      int64_t z = j;
+      while (z < len && idx[z] == s) ++z;
+      if (s >= 0 && s < segs) {
+        for (int64_t f = 0; f < feat; ++f) {
+          int64_t v, where = len, start = j;
+          if (reduce <= 1) {
+            v = (reduce == 1 && has_out) ? o[s * feat + f] : 0; /* exact (64-bit) sum */
+          } else if (has_out) {
+            v = o[s * feat + f];
+          } else {
+            v = src[(b * len + j) * feat + f];
+            where = j;
+            start = j + 1;
+          }
+          for (int64_t t = (reduce <= 1 ? j : start); t < z; ++t) {
+            const int64_t x = src[(b * len + t) * feat + f];
+            if (reduce <= 1) v = (int64_t)((uint64_t)v + (uint64_t)x);
+            else if (reduce == 2 ? x <= v : x >= v) {
+              v = x;
+              where = t;
+            }
+          }
+          if (reduce == 1) {
+            const int64_t c = narrow(z - j, bits, is_unsigned);
+            v = c != 0 ? trunc_div(narrow(v, bits, is_unsigned), c) : trunc_div(v, z - j);
+          }
+          o[s * feat + f] = narrow(v, bits, is_unsigned);
+          if (ag && reduce >= 2) ag[s * feat + f] = where;
+        }
+      }
+      j = z;
+    }
+  }
+}
+
+/* scatter, reference test/scatter/arch35/golden.py:49-127: in-order fold into
+ * typed out cells (each += / *= wraps in the dtype), min/max with <= / >=
+ * from out or the dtype's limits (untouched cells -> 0 without out), and the
+ * mean's finish (golden :106-118, python/ops_gnn/scatter.py:443-456): where
+ * the count is non-zero, floor division by the count, which for 8/16-bit
+ * dtypes is first narrowed to the dtype and clamped to >= 1.  reduce codes:
+ * 0 sum 1 mean 2 min 3 max 4 prod. */
+void oracle_int_scatter(const int64_t* src, const int64_t* index, int64_t before, int64_t len, int64_t after,
+                        int64_t size, int reduce, int has_out, int bits, int is_unsigned, int64_t* out,
+                        int64_t* arg) {
+  const int64_t total = before * size * after;
+  int64_t* count = reduce == 1 ? (int64_t*)calloc((size_t)(total > 0 ? total : 1), sizeof(int64_t)) : 0;
+  for (int64_t i = 0; i < total; ++i) {
+    if (!has_out)
+      out[i] = reduce == 4 ? 1 : reduce == 2 ? int_limit(bits, is_unsigned, 1)
+             : reduce == 3 ? int_limit(bits, is_unsigned, 0) : 0;
+    if (arg) arg[i] = len;
+  }
+  for (int64_t b = 0; b < before; ++b)
+    for (int64_t l = 0; l < len; ++l)
+      for (int64_t f = 0; f < after; ++f) {
+        const int64_t t = index[(b * len + l) * after + f];
+        if (t < 0 || t >= size) continue;
+        const int64_t x = src[(b * len + l) * after + f];
+        const int64_t key = (b * size + t) * after + f;
+        if (reduce == 0 || reduce == 1) {
+          out[key] = narrow((int64_t)((uint64_t)out[key] + (uint64_t)x), bits, is_unsigned);
+          if (count) count[key] += 1;
+        } else if (reduce == 4) {
+          out[key] = narrow((int64_t)((uint64_t)out[key] * (uint64_t)x), bits, is_unsigned);
+        } else if (reduce == 2 ? x <= out[key] : x >= out[key]) {
+          out[key] = x;
+          if (arg) arg[key] = l;
+        }
+      }
+  if (count) {
+    for (int64_t i = 0; i < total; ++i) {
+      if (count[i] <= 0) continue;
+      int64_t d = count[i];
+      if (bits <= 16) {
+        d = narrow(d, bits, is_unsigned);
+        if (d < 1) d = 1;
+      }
+      out[i] = narrow(floor_div(out[i], d), bits, is_unsigned);
+    }
+    free(count);
+  }
+  if (!has_out && (reduce == 2 || reduce == 3) && arg) {
+    for (int64_t i = 0; i < total; ++i)
+      if (arg[i] == len) out[i] = 0;
+  }
 }

@@ -52,6 +52,11 @@ def lib():
                                          ctypes.c_int, _f64p, vp]
         l.oracle_scatter.argtypes = [_f32p, _i64p, i64, i64, i64, i64, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_double, _f64p, vp]
+        l.oracle_scatter_f64.argtypes = [_f64p, _i64p, i64, i64, i64, i64, ctypes.c_int, ctypes.c_int, _f64p, vp]
+        ci = ctypes.c_int
+        l.oracle_int_segment_csr.argtypes = [_i64p, _i64p, i64, i64, i64, i64, i64, ci, ci, ci, _i64p, vp]
+        l.oracle_int_segment_coo.argtypes = [_i64p, _i64p, i64, i64, i64, i64, i64, ci, ci, ci, ci, _i64p, vp]
+        l.oracle_int_scatter.argtypes = [_i64p, _i64p, i64, i64, i64, i64, ci, ci, ci, ci, _i64p, vp]
         l.oracle_segment_lse.argtypes = [_f32p, _i64p, i64, i64, i64, i64, i64, _f64p]
         l.oracle_group_softmax.argtypes = [_f32p, _i64p, i64, i64, i64, i64, ctypes.c_int, _f64p]
         u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
@@ -69,13 +74,30 @@ def lib():
 def _np(x, dtype=None):
     if hasattr(x, "detach"):  # torch tensor
         x = x.detach().cpu()
-        if dtype is not None and x.is_floating_point():
-            x = x.float()
+        if dtype is not None and x.is_floating_point() and x.dtype != __import__("torch").float64:
+            x = x.float()  # fp16 / bf16 widen exactly; numpy has no bf16
         x = x.numpy()
     x = np.asarray(x)
     if dtype is not None:
         x = x.astype(dtype, copy=False)
     return np.ascontiguousarray(x)
+
+
+def _int_kind(x):
+    """(bits, is_unsigned) of an integer array / tensor, or None for floats."""
+    dt = x.dtype
+    if hasattr(x, "detach"):  # torch dtype -> numpy dtype
+        if dt.is_floating_point or dt.is_complex or dt == __import__("torch").bool:
+            return None
+        dt = np.dtype(str(dt).replace("torch.", ""))
+    dt = np.dtype(dt)
+    if dt.kind not in "iu":
+        return None
+    return dt.itemsize * 8, int(dt.kind == "u")
+
+
+def _is_f64(x):
+    return str(x.dtype) in ("float64", "torch.float64")
 
 
 def _ptr(a):
@@ -129,10 +151,12 @@ def ptr2ind(ptr, numel):
 def segment_csr(src, indptr, reduce="sum"):
     """segment_csr golden (reference test/segment_csr/arch35/golden.py:21-103).
 
-    Returns (values float64, arg int64 or None).  Reduction axis is
-    indptr.dim() - 1; leading indptr dims broadcast to src's.
+    Returns (values float64 -- int64 already wrapped to the dtype for integer
+    src --, arg int64 or None).  Reduction axis is indptr.dim() - 1; leading
+    indptr dims broadcast to src's.
     """
-    src = _np(src, np.float32)
+    kind = _int_kind(src)
+    src = _np(src, np.int64 if kind else np.float32)
     ip = _np(indptr, np.int64)
     dim = ip.ndim - 1
     lead = src.shape[:dim]
@@ -148,8 +172,13 @@ def segment_csr(src, indptr, reduce="sum"):
         stride = 0
     r = REDUCE[reduce]
     shape = lead + (segs,) + src.shape[dim + 1:]
-    out = np.zeros(shape, dtype=np.float64)
     arg = np.zeros(shape, dtype=np.int64) if r >= 2 else None
+    if kind:
+        out = np.zeros(shape, dtype=np.int64)
+        lib().oracle_int_segment_csr(np.ascontiguousarray(src.reshape(-1)), ip.reshape(-1), stride, batch, length,
+                                     feat, segs, r, kind[0], kind[1], out, _ptr(arg))
+        return out, arg
+    out = np.zeros(shape, dtype=np.float64)
     lib().oracle_segment_csr(np.ascontiguousarray(src.reshape(-1)), ip.reshape(-1), stride, batch,
                              length, feat, segs, r, out, _ptr(arg))
     return out, arg
@@ -171,7 +200,8 @@ def segment_coo(src, index, segments, reduce="sum", out=None):
     leading dims 1 or equal to src's.  out: optional seed values (float64
     array of the output shape).  Returns (values float64, arg int64 | None).
     """
-    src = _np(src, np.float32)
+    kind = _int_kind(src)
+    src = _np(src, np.int64 if kind else np.float32)
     idx = _np(index, np.int64)
     dim = idx.ndim - 1
     before, length, after = _split(src.shape, dim)
@@ -180,8 +210,14 @@ def segment_coo(src, index, segments, reduce="sum", out=None):
         raise ValueError("index leading dims must broadcast")
     r = REDUCE[reduce]
     shape = src.shape[:dim] + (segments,) + src.shape[dim + 1:]
-    o = np.zeros(shape, np.float64) if out is None else np.array(out, dtype=np.float64).reshape(shape).copy()
     arg = np.zeros(shape, np.int64) if r >= 2 else None
+    if kind:
+        o = np.zeros(shape, np.int64) if out is None else _np(out, np.int64).reshape(shape).copy()
+        lib().oracle_int_segment_coo(np.ascontiguousarray(src.reshape(-1)), np.ascontiguousarray(idx.reshape(-1)),
+                                     ib, before, length, after, segments, r, 0 if out is None else 1, kind[0],
+                                     kind[1], o, _ptr(arg))
+        return o, arg
+    o = np.zeros(shape, np.float64) if out is None else np.array(out, dtype=np.float64).reshape(shape).copy()
     lib().oracle_segment_coo(np.ascontiguousarray(src.reshape(-1)), np.ascontiguousarray(idx.reshape(-1)), ib,
                              before, length, after, segments, r, 0 if out is None else 1, o, _ptr(arg))
     return o, arg
@@ -193,14 +229,26 @@ def scatter(src, index, dim, size, reduce="sum", out=None, dtype_name="float32")
     index must already have src's shape (broadcast by the caller).  reduce
     codes as torch_scatter: sum/add/mean/min/max/mul.  Returns (values, arg|None).
     """
-    src = _np(src, np.float32)
+    kind = _int_kind(src)
+    f64 = _is_f64(src)
+    src = _np(src, np.int64 if kind else (np.float64 if f64 else np.float32))
     idx = np.ascontiguousarray(np.broadcast_to(_np(index, np.int64), src.shape))
     before, length, after = _split(src.shape, dim)
     code = {"sum": 0, "add": 0, "mean": 1, "min": 2, "max": 3, "mul": 4}[reduce]
     shape = src.shape[:dim] + (size,) + src.shape[dim + 1:]
-    o = np.zeros(shape, np.float64) if out is None else np.array(out, dtype=np.float64).reshape(shape).copy()
     arg = np.zeros(shape, np.int64) if code in (2, 3) else None
-    lib().oracle_scatter(np.ascontiguousarray(src.reshape(-1)), idx.reshape(-1), before, length, after, size,
+    flat = np.ascontiguousarray(src.reshape(-1))
+    if kind:
+        o = np.zeros(shape, np.int64) if out is None else _np(out, np.int64).reshape(shape).copy()
+        lib().oracle_int_scatter(flat, idx.reshape(-1), before, length, after, size, code, 0 if out is None else 1,
+                                 kind[0], kind[1], o, _ptr(arg))
+        return o, arg
+    o = np.zeros(shape, np.float64) if out is None else _np(out, np.float64).reshape(shape).copy()
+    if f64:
+        lib().oracle_scatter_f64(flat, idx.reshape(-1), before, length, after, size, code,
+                                 0 if out is None else 1, o, _ptr(arg))
+        return o, arg
+    lib().oracle_scatter(flat, idx.reshape(-1), before, length, after, size,
                          code, 0 if out is None else 1, FINFO_MAX[dtype_name], o, _ptr(arg))
     return o, arg
 
