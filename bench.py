@@ -407,7 +407,8 @@ def bench_gat(args):
            "softmax": 2 * e + 2 * e + 8 * e,
            "spmm": 8 * e + 2 * e + 2 * e * f + 2 * n * f + 8 * (n + 1)}
     comp = {"sddmm": 8 * e + 2 * e + 2 * 2 * n * f + 8 * (n + 1),
-            "softmax": eff["softmax"],
+            # the sorted-index fused pass reads the cached row pointers, not the index
+            "softmax": 2 * e + 2 * e + 8 * (n + 1),
             "spmm": 8 * e + 2 * e + 2 * 2 * n * f + 8 * (n + 1)}
     ops = {}
     with torch.no_grad():
@@ -419,7 +420,7 @@ def bench_gat(args):
             log(f"bench gat {name}: {ms:.4f} ms, effective {eff[name] / ms / 1e6:.1f} GB/s, "
                 f"compulsory {comp[name] / ms / 1e6:.1f} GB/s")
         ms = _timed(layer, args.steps, args.warmup)
-        km = _kernel_ms(layer, args.steps, ["sddmm_main", "spmm_main", "group_apply", "segment_stats_main"])
+        km = _kernel_ms(layer, args.steps, ["sddmm_main", "spmm_main", "segment_softmax", "group_apply", "segment_stats_main"])
     tot_eff = sum(eff.values())
     ops["layer"] = {"ms": round(ms, 4), "kernels_ms": {k2: round(v2, 4) for k2, v2 in km.items()}}
     log(f"bench gat layer: {ms:.4f} ms; kernels {km}")

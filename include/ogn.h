@@ -250,6 +250,20 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
                             int64_t segments, int64_t k, float* m_out, float* s_out, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* Fused softmax (log_softmax = 0) or log_softmax (1) of one-feature rows:
+ * src / out [batch, length] (the per-edge score layout, after = 1), row r of
+ * every batch = positions [indptr[r], indptr[r+1]) (shared indptr
+ * [segments + 1]).  out = exp(x - clamp(m)) / s or (x - clamp(m)) - log(s)
+ * with (m, s) as ogn_segment_group_stats; a row holding +inf is NaN
+ * throughout.  Positions outside [indptr[0], indptr[segments]) are not
+ * written.  16, 32 or 64 lanes per row (by the average row length): meant
+ * for rows of >= ~64 positions on average.  src and out 16-byte aligned, and length * element size a
+ * multiple of 16 when batch > 1.  No workspace.  Fuses the sorted-index
+ * forward phases of scatter_softmax / scatter_log_softmax (reference
+ * csrc/npu/scatter_softmax/common/grouped_softmax_shared.h:178-209). */
+int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
+                              int64_t segments, void* out, int log_softmax, void* stream);
+
 /* ------------------------------------------------------------------ unsorted scatter
  * torch_scatter scatter with an arbitrary int64 index (same rules as
  * OGN_SEM_SCATTER above).  src: [before, len, after] contiguous; index read

@@ -66,6 +66,141 @@ __global__ __launch_bounds__(256) void index_facts_kernel(const int64_t* __restr
   }
 }
 
+// One-feature rows (k == 1) that are long on average: one wavefront per
+// (batch, row).  Lanes read the row as aligned 16-byte packets (8 fp16/bf16
+// or 4 fp32 positions), fold each packet into the log-sum-exp state (m, s)
+// with one rescale, and merge the 64 lane states in a butterfly (fmax and +
+// commute, so every lane ends with the same bits).  The general engine
+// spreads one-feature rows over 64 lanes with one 2-byte load each; here
+// every load is a full packet, and only the two packets a row shares with
+// its neighbours pay for per-position masks.
+template <int DT>
+__device__ __forceinline__ void load_packet(const typename Elem<DT>::S* row, int64_t q, int64_t rs, int64_t re,
+                                            int64_t length, float* x) {
+  using E = Elem<DT>;
+  constexpr int V = E::VEC;
+  if (q >= rs && q + V <= re) {  // interior packet (re <= length)
+    E::unpack(*reinterpret_cast<const uint4*>(row + q), x);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i)  // outside the row: -inf, exp(-inf) = 0
+    x[i] = (q + i >= rs && q + i < re) ? E::load1(row, q + i) : -__builtin_inff();
+}
+
+template <int DT>
+__device__ __forceinline__ void row_lse_k1(const typename Elem<DT>::S* row, int64_t rs, int64_t re, int64_t length,
+                                           float& m, float& sacc) {
+  constexpr int V = Elem<DT>::VEC;
+  m = -__builtin_inff();
+  sacc = 0.f;
+#pragma unroll 2
+  for (int64_t q = rs / V * V + (int64_t)lane_id() * V; q < re; q += (int64_t)kWave * V) {
+    float x[V];
+    load_packet<DT>(row, q, rs, re, length, x);
+    float pm = m;
+#pragma unroll
+    for (int i = 0; i < V; ++i) pm = fmaxf(pm, x[i]);  // NaN-ignoring, as lse_add
+    const float cn = clampf_max(pm);
+    float t = sacc * fast_exp(clampf_max(m) - cn);
+#pragma unroll
+    for (int i = 0; i < V; ++i) t += fast_exp(x[i] - cn);
+    m = pm;
+    sacc = t;
+  }
+  auto merge = [&](auto offc) {
+    constexpr int off = decltype(offc)::value;
+    const float om = xor_shfl<off>(m), os = xor_shfl<off>(sacc);
+    lse_merge(m, sacc, om, os);
+  };
+  merge(std::integral_constant<int, 1>{});
+  merge(std::integral_constant<int, 2>{});
+  merge(std::integral_constant<int, 4>{});
+  merge(std::integral_constant<int, 8>{});
+  merge(std::integral_constant<int, 16>{});
+  merge(std::integral_constant<int, 32>{});
+}
+
+// 4 wavefronts per block, one row each.
+template <int DT>
+__global__ __launch_bounds__(256) void row_stats_k1_kernel(const int64_t* __restrict__ ptr, const void* __restrict__ src,
+                                                           int64_t length, int64_t segments, float* __restrict__ m_out,
+                                                           float* __restrict__ s_out) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= segments) return;
+  const int64_t b = blockIdx.y;
+  const int64_t rs = std::max<int64_t>(ptr[r], 0);
+  const int64_t re = std::min<int64_t>(ptr[r + 1], length);
+  float m, sacc;
+  row_lse_k1<DT>(static_cast<const typename Elem<DT>::S*>(src) + b * length, rs, re, length, m, sacc);
+  if (lane_id() == 0) {
+    m_out[b * segments + r] = m;
+    s_out[b * segments + r] = sacc;
+  }
+}
+
+// Fused softmax / log_softmax of one-feature rows: the statistics as above,
+// then a second pass over the row (just read, so served by the caches) that
+// writes exp(x - clamp(m)) / s or (x - clamp(m)) - log(s); a row holding
+// +inf gives NaN throughout (torch.softmax).  Packets shared with a
+// neighbouring row are written element by element.
+template <int DT>
+__global__ __launch_bounds__(256) void row_softmax_k1_kernel(const int64_t* __restrict__ ptr,
+                                                             const void* __restrict__ src, int64_t length,
+                                                             int64_t segments, void* __restrict__ out, int log_mode) {
+  using E = Elem<DT>;
+  constexpr int V = E::VEC;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= segments) return;
+  const int64_t b = blockIdx.y;
+  const int64_t rs = std::max<int64_t>(ptr[r], 0);
+  const int64_t re = std::min<int64_t>(ptr[r + 1], length);
+  const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
+  float m, sacc;
+  row_lse_k1<DT>(row, rs, re, length, m, sacc);
+  const float cm = clampf_max(m);
+  const float ls = logf(sacc);
+  const float inv = 1.f / sacc;
+  const bool poisoned = m == __builtin_inff();
+#pragma unroll 2
+  for (int64_t q = rs / V * V + (int64_t)lane_id() * V; q < re; q += (int64_t)kWave * V) {
+    float x[V], v[V];
+    load_packet<DT>(row, q, rs, re, length, x);
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      v[i] = log_mode ? (x[i] - cm) - ls : fast_exp(x[i] - cm) * inv;
+    if (poisoned) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[i] = __builtin_nanf("");
+    }
+    const int64_t o = b * length + q;
+    if (q >= rs && q + V <= re) {
+      store_floats<V, true>(out, DT, o, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        if (q + i >= rs && q + i < re) store_floats<1>(out, DT, o + i, &v[i]);
+    }
+  }
+}
+
+template <int DT>
+void launch_row_kernel(bool softmax, dim3 grid, hipStream_t st, const int64_t* ptr, const void* src, int64_t length,
+                       int64_t segments, float* m, float* s, void* out, int lm) {
+  if (softmax)
+    hipLaunchKernelGGL(row_softmax_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, out, lm);
+  else
+    hipLaunchKernelGGL(row_stats_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, m, s);
+}
+
+void launch_rows(bool softmax, int dtype, int64_t batch, hipStream_t st, const int64_t* ptr, const void* src,
+                 int64_t length, int64_t segments, float* m, float* s, void* out, int lm) {
+  const dim3 grid((unsigned)((segments + 3) / 4), (unsigned)batch);
+  if (dtype == OGN_F32) launch_row_kernel<OGN_F32>(softmax, grid, st, ptr, src, length, segments, m, s, out, lm);
+  else if (dtype == OGN_F16) launch_row_kernel<OGN_F16>(softmax, grid, st, ptr, src, length, segments, m, s, out, lm);
+  else launch_row_kernel<OGN_BF16>(softmax, grid, st, ptr, src, length, segments, m, s, out, lm);
+}
+
 }  // namespace
 
 extern "C" {
@@ -158,6 +293,15 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
   if (batch == 0 || segments == 0 || k == 0) return OGN_OK;
   if (!indptr || !m_out || !s_out || (length > 0 && !src))
     return fail(OGN_EINVAL, "ogn_segment_group_stats: null pointer");
+  // One-feature rows that average >= 64 positions: whole wavefronts per row.
+  const int esize = dtype_size(dtype);
+  if (k == 1 && length >= 64 * segments && is_aligned(src, 16) && (batch == 1 || (length * esize) % 16 == 0) &&
+      batch <= 65535) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    TimedLaunch t("segment_stats_main", st);
+    launch_rows(false, dtype, batch, st, indptr, src, length, segments, m_out, s_out, nullptr, 0);
+    return check_launch("ogn_segment_group_stats");
+  }
   const bool aligned = is_aligned(src, 16) && is_aligned(m_out, 16);
   const Plan pl = make_plan(length, k, dtype, aligned);
   Params p{};
@@ -177,6 +321,22 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
   p.arg_empty = length;
   return run(pl, p, dtype, OGN_I64, false, RK_LSE, batch, workspace, workspace_bytes,
              static_cast<hipStream_t>(stream), "segment_stats");
+}
+
+int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
+                              int64_t segments, void* out, int log_softmax, void* stream) {
+  if (batch < 0 || length < 0 || segments < 0) return fail(OGN_EINVAL, "ogn_segment_group_softmax: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_segment_group_softmax: src dtype must be float32, float16 or bfloat16");
+  if (batch == 0 || segments == 0 || length == 0) return OGN_OK;
+  if (!indptr || !src || !out) return fail(OGN_EINVAL, "ogn_segment_group_softmax: null pointer");
+  if (!is_aligned(src, 16) || !is_aligned(out, 16) || (batch > 1 && (length * dtype_size(dtype)) % 16 != 0))
+    return fail(OGN_EINVAL, "ogn_segment_group_softmax: src / out rows must be 16-byte aligned");
+  if (batch > 65535) return fail(OGN_EUNSUPPORTED, "ogn_segment_group_softmax: batch > 65535");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TimedLaunch t("segment_softmax", st);
+  launch_rows(true, dtype, batch, st, indptr, src, length, segments, nullptr, nullptr, out, log_softmax ? 1 : 0);
+  return check_launch("ogn_segment_group_softmax");
 }
 
 int ogn_ind2ptr_batched(const int64_t* ind, int64_t batches, int64_t numel, int64_t rows, int64_t* out,

@@ -205,6 +205,40 @@ def scatter_atomic(src3: torch.Tensor, index: torch.Tensor, strides, size: int, 
     return arg
 
 
+_SORTED_PTR = _VersionCache()
+
+
+def sorted_index_ptr(index: torch.Tensor, groups: int) -> torch.Tensor:
+    """Group pointers [1, groups + 1] of a sorted 1-D index, cached per
+    index version (and group count)."""
+    def compute():
+        return (groups, ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups))
+    hit = _SORTED_PTR.get(index, compute)
+    if hit[0] != groups:
+        _SORTED_PTR.clear()
+        hit = _SORTED_PTR.get(index, compute)
+    return hit[1]
+
+
+def fused_row_softmax_ok(src3: torch.Tensor, groups: int) -> bool:
+    """The one-wavefront-per-row fused softmax applies: one feature, rows
+    averaging >= 64 positions, 16-byte aligned rows."""
+    b, length, f = src3.shape
+    return (f == 1 and groups > 0 and length >= 64 * groups and src3.data_ptr() % 16 == 0
+            and (b == 1 or (length * src3.element_size()) % 16 == 0) and b <= 65535)
+
+
+def group_softmax_rows(src3: torch.Tensor, ptr: torch.Tensor, groups: int, log_softmax: bool) -> torch.Tensor:
+    b, length, _ = src3.shape
+    out = torch.empty_like(src3)
+    if out.numel() == 0:
+        return out
+    rc = lib.ogn_segment_group_softmax(dptr(ptr), dptr(src3), _lib.TORCH_TO_OGN[src3.dtype], b, length, groups,
+                                       dptr(out), 1 if log_softmax else 0, stream_of(src3))
+    check(rc, "grouped softmax")
+    return out
+
+
 def group_stats(src3: torch.Tensor, index: torch.Tensor, groups: int, sorted_index: bool
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-(batch, group, feature) max and sum(exp(x - clamp(max))), fp32."""
@@ -215,7 +249,7 @@ def group_stats(src3: torch.Tensor, index: torch.Tensor, groups: int, sorted_ind
         return m, s
     code = _lib.TORCH_TO_OGN[src3.dtype]
     if sorted_index:
-        ptr = ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups)
+        ptr = sorted_index_ptr(index, groups)
         ws_bytes = lib.ogn_segment_reduce_workspace_size(b, length, groups, f, 1, code, _lib.R_LSE)
         ws = _lib.workspace(ws_bytes, src3.device)
         rc = lib.ogn_segment_group_stats(dptr(ptr), dptr(src3), code, b, length, groups, f, dptr(m), dptr(s),

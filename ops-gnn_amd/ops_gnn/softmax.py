@@ -11,7 +11,9 @@ Forward, all HIP: per-(batch, group, feature) statistics m = max and
 s = sum(exp(x - clamp(m))) -- from the contiguous-segment engine when the
 index is sorted (deterministic), from atomics otherwise -- then one
 elementwise pass (softmax / log_softmax) or one pass over the groups
-(logsumexp).  fp32 math for every dtype.
+(logsumexp).  A sorted index over one-feature rows that average >= 64
+positions (per-edge attention scores) takes one fused kernel, a wavefront
+per row, instead.  fp32 math for every dtype.
 
 Backward (reference python/ops_gnn/_grouped_softmax.py:102-133,
 scatter_logsumexp.py:57-84), all HIP: softmax out * (g - sum_group(out * g)),
@@ -101,8 +103,12 @@ class _GroupedSoftmax(torch.autograd.Function):
     @staticmethod
     def forward(ctx, src, index, groups, is_sorted, log_softmax, shape3):
         src3 = src.contiguous().reshape(shape3)
-        m, s = _stats(src3, index, groups, is_sorted)
-        out3 = _native.group_softmax_apply(src3, index, groups, m, s, log_softmax)
+        if is_sorted and _native.fused_row_softmax_ok(src3, groups):
+            # one feature per position, long rows: statistics and output in one pass per row
+            out3 = _native.group_softmax_rows(src3, _native.sorted_index_ptr(index, groups), groups, log_softmax)
+        else:
+            m, s = _stats(src3, index, groups, is_sorted)
+            out3 = _native.group_softmax_apply(src3, index, groups, m, s, log_softmax)
         ctx.save_for_backward(out3, index)
         ctx.groups, ctx.log_softmax, ctx.shape3 = groups, log_softmax, src3.shape
         return out3.reshape(src.shape)
@@ -123,7 +129,7 @@ class _GroupedLogSumExp(torch.autograd.Function):
     def forward(ctx, src, index, groups, is_sorted, shape3, shape):
         src3 = src.contiguous().reshape(shape3)
         if is_sorted:
-            ptr = _native.ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups)
+            ptr = _native.sorted_index_ptr(index, groups)
             res3, _ = _native.segment_reduce(src3, ptr, groups, _lib.R_LSE, _lib.SEM_SEGMENT_CSR)
         else:
             m, s = _stats(src3, index, groups, False)

@@ -185,6 +185,28 @@ def test_grouped_softmax_edge_rows(ogn, oracle, mode):
     _softmax_check(ogn, oracle, src, torch.from_numpy(idx), 0, 500, mode, 1e-5)
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+@pytest.mark.parametrize("before", [1, 2])
+@pytest.mark.parametrize("mean_len", [90, 300, 1200])
+def test_grouped_softmax_long_edge_rows(ogn, oracle, dtype, mode, before, mean_len):
+    # one score per edge, rows averaging >= 128 edges (the GAT regime of
+    # config 4): the row-per-wavefront statistics kernel; rows start at
+    # arbitrary (unaligned) positions, some are empty, some hold +-inf / NaN
+    rng = np.random.default_rng(53)
+    deg = np.maximum(rng.lognormal(np.log(mean_len) - 0.5, 1.0, 300).astype(np.int64), 1)
+    deg[[3, 77, 150]] = 0
+    deg[10] = 30 * mean_len
+    idx = np.repeat(np.arange(300), deg)
+    x = (rng.standard_normal((before, idx.size)) * 4).astype(np.float32)
+    starts = np.concatenate([[0], np.cumsum(deg)])
+    x[0, starts[20] + 5] = INF
+    x[0, starts[21]:starts[22]] = -INF
+    x[-1, starts[30] + 1] = NAN
+    src = torch.from_numpy(x).to(dtype)
+    _softmax_check(ogn, oracle, src, torch.from_numpy(idx), 1, 300, mode, SOFT_TOL[dtype])
+
+
 @pytest.mark.parametrize("sorted_index", [True, False])
 def test_grouped_softmax_special_values(ogn, oracle, sorted_index):
     src = torch.tensor([INF, 1.0, -INF, 2.0, NAN, 0.0, -INF, -INF])
