@@ -248,3 +248,63 @@ def test_segment_logsumexp_errors(ogn):
         ogn.segment_logsumexp(src, torch.tensor([0, 3], device="cuda"))
     with pytest.raises(TypeError):
         ogn.segment_logsumexp(src.double(), torch.tensor([0, 4], device="cuda"))
+
+
+# ------------------------------------------------------------------ mixed short / hub rows
+def _mixed_lengths(rng, segs, hub):
+    """Config-5-like rows: mostly 1-3 positions (chunks of them take the
+    short-row kernel), a few medium rows, and one hub row that spans many
+    chunks (folded by the fix-up across its lane groups)."""
+    lengths = np.minimum(rng.zipf(1.8, size=segs), 300)
+    lengths[rng.integers(0, segs, segs // 20)] = 0
+    lengths[segs // 3] = hub
+    return lengths
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("reduce", REDUCES)
+@pytest.mark.parametrize("feat", [1, 4, 32, 33, 128])
+def test_segment_csr_short_rows_and_hub(ogn, oracle, dtype, reduce, feat):
+    rng = np.random.default_rng(100 + feat)
+    lengths = _mixed_lengths(rng, 4000, 60000 if feat <= 4 else 9000)
+    src = torch.from_numpy(rng.standard_normal((int(lengths.sum()), feat)).astype(np.float32)).to(dtype)
+    if reduce in ("min", "max"):
+        src = torch.from_numpy(rng.integers(-3, 4, size=tuple(src.shape)).astype(np.float32)).to(dtype)  # ties
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)]))
+    _csr_check(ogn, oracle, src, indptr, reduce, f"mixed/{dtype}/{reduce}/f{feat}")
+
+
+@pytest.mark.parametrize("reduce", REDUCES)
+@pytest.mark.parametrize("with_out", [False, True])
+@pytest.mark.parametrize("feat", [1, 32])
+def test_segment_coo_short_rows_and_hub(ogn, oracle, reduce, with_out, feat):
+    # later-tie rule and seeds on the short-row kernel and the grouped fix-up
+    rng = np.random.default_rng(7 + feat)
+    lengths = _mixed_lengths(rng, 3000, 40000)
+    index = np.repeat(np.arange(3000), lengths)
+    src = torch.from_numpy(rng.integers(-3, 4, size=(index.size, feat)).astype(np.float32))
+    out = torch.from_numpy(rng.integers(-3, 4, size=(3000, feat)).astype(np.float32)) if with_out else None
+    fn = getattr(ogn, f"segment_{reduce}_coo")
+    res = fn(src.cuda(), torch.from_numpy(index).cuda(), None if out is None else out.clone().cuda(), 3000)
+    got, arg = res if isinstance(res, tuple) else (res, None)
+    gold, garg = oracle.segment_coo(src, index, 3000, reduce, None if out is None else out.double().numpy())
+    if arg is not None:
+        assert_exact(got, gold, "coo values")
+        assert_exact(arg, garg, "coo arg")
+    else:
+        scale, _ = oracle.segment_coo(src.abs(), index, 3000, reduce,
+                                      None if out is None else out.double().abs().numpy())
+        assert_sum_close(got, gold, scale, torch.float32, "coo")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("feat", [1, 32])
+def test_segment_logsumexp_short_rows_and_hub(ogn, oracle, dtype, feat):
+    rng = np.random.default_rng(9)
+    lengths = _mixed_lengths(rng, 3000, 40000)
+    src = torch.from_numpy((rng.standard_normal((int(lengths.sum()), feat)) * 3).astype(np.float32)).to(dtype)
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)]))
+    got = ogn.segment_logsumexp(src.cuda(), indptr.cuda())
+    gold = oracle.segment_logsumexp(src, indptr)
+    g = got.float().cpu().numpy()
+    np.testing.assert_allclose(g, cast_like(gold, dtype), rtol=LSE_TOL[dtype], atol=LSE_TOL[dtype])
