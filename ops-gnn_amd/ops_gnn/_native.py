@@ -164,6 +164,16 @@ class _VersionCache:
             self._d.popitem(last=False)
         return value
 
+    def put(self, t, value):
+        import weakref
+        try:
+            key = (id(t), t.data_ptr(), tuple(t.shape), tuple(t.stride()), t._version)
+        except (AttributeError, RuntimeError):
+            return
+        self._d[key] = (weakref.ref(t), value)
+        if len(self._d) > self._limit:
+            self._d.popitem(last=False)
+
     def clear(self):
         self._d.clear()
 
@@ -208,16 +218,22 @@ def scatter_atomic(src3: torch.Tensor, index: torch.Tensor, strides, size: int, 
 _SORTED_PTR = _VersionCache()
 
 
-def sorted_index_ptr(index: torch.Tensor, groups: int) -> torch.Tensor:
-    """Group pointers [1, groups + 1] of a sorted 1-D index, cached per
-    index version (and group count)."""
+def sorted_index_ptr(index: torch.Tensor, groups: int, index2d: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Group pointers [B, groups + 1] of a sorted index (index2d [B, L], by
+    default `index` as one row), cached per version of the caller's `index`
+    (and group count and shape): repeated calls with the same index skip the
+    batched ind2ptr."""
+    rows2d = index.reshape(1, -1) if index2d is None else index2d
+    shape = tuple(rows2d.shape)
+
     def compute():
-        return (groups, ind2ptr_batched(index.to(torch.int64).reshape(1, -1), groups))
+        return (groups, shape, ind2ptr_batched(rows2d.to(torch.int64).contiguous(), groups))
+
     hit = _SORTED_PTR.get(index, compute)
-    if hit[0] != groups:
-        _SORTED_PTR.clear()
-        hit = _SORTED_PTR.get(index, compute)
-    return hit[1]
+    if hit[0] != groups or hit[1] != shape:
+        hit = compute()
+        _SORTED_PTR.put(index, hit)
+    return hit[2]
 
 
 def fused_row_softmax_ok(src3: torch.Tensor, groups: int) -> bool:

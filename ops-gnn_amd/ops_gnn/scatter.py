@@ -122,7 +122,7 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
         is_sorted, mn, mx = _native.index_facts(line, key=index)
         use_segments = is_sorted and mn >= 0 and mx < size
     if use_segments:
-        ptr = _native.ind2ptr_batched(line.contiguous().reshape(1, -1), size)
+        ptr = _native.sorted_index_ptr(index, size, line.reshape(1, -1))
         res3, arg3 = _native.segment_reduce(src3, ptr, size, code, _lib.SEM_SCATTER, out3, has_out, is_minmax)
     else:
         if compact:

@@ -187,6 +187,23 @@ def segment_max_csr_legacy(src: torch.Tensor, indptr: torch.Tensor, optional_out
 
 
 # ------------------------------------------------------------------ segment_coo
+_COO_FACTS = _native._VersionCache()
+
+
+def _coo_index_facts(index: torch.Tensor):
+    """(min, max, sorted along the last dim) of a COO index, one small
+    device-to-host read cached per index version (reference
+    csrc/npu/segment_coo/op_host/segment_coo.cpp:65-109 ValidateIndex)."""
+    def compute():
+        if index.dim() == 1:
+            ok, mn, mx = _native.index_facts(index)
+            return mn, mx, ok
+        bad = (index[..., 1:] < index[..., :-1]).any() if index.size(-1) > 1 else index.new_zeros((), dtype=torch.bool)
+        mn, mx, uns = torch.stack((index.min(), index.max(), bad.to(torch.int64))).tolist()
+        return mn, mx, uns == 0
+    return _COO_FACTS.get(index, compute)
+
+
 def _segment_coo(src, index, out, dim_size, reduce, return_arg):
     _lib.require_gpu(src, index, what="segment_coo")
     if index.dtype != torch.int64:
@@ -201,12 +218,21 @@ def _segment_coo(src, index, out, dim_size, reduce, return_arg):
         if index.size(i) not in (1, src.size(i)) or (i == dim and index.size(i) != src.size(i)):
             raise ValueError("index shape must broadcast to src")
     before, length, after = _split(src.shape, dim)
+    facts = _coo_index_facts(index) if index.numel() else None
+    if facts is not None:
+        # the reference's checks and messages (segment_coo.cpp:97-100)
+        if facts[0] < 0:
+            raise RuntimeError("index values must be non-negative")
+        if not facts[2]:
+            raise RuntimeError("index must be sorted along its last dimension")
     if out is not None:
         segs = out.size(dim)
     elif dim_size is not None:
         segs = int(dim_size)
     else:
-        segs = (_native.index_facts(index)[2] + 1) if index.numel() else 0
+        segs = facts[1] + 1 if facts is not None else 0
+    if facts is not None and (out is not None or dim_size is not None) and facts[1] >= segs:
+        raise RuntimeError("index values exceed output size")
     shape = list(src.shape)
     shape[dim] = segs
     out = _prepare_out(out, shape, src, "segment_coo")
@@ -217,7 +243,7 @@ def _segment_coo(src, index, out, dim_size, reduce, return_arg):
     if src.numel() == 0 or segs == 0:
         res = out if out is not None else torch.zeros(shape, dtype=src.dtype, device=src.device)
         return res, torch.full(shape, length, dtype=torch.int64, device=src.device)
-    ptr2d = _native.ind2ptr_batched(idx2d.contiguous(), segs)
+    ptr2d = _native.sorted_index_ptr(index, segs, idx2d)
     src3 = src.contiguous().reshape(before, length, after)
     has_out = out is not None
     direct = has_out and out.is_contiguous()

@@ -214,6 +214,29 @@ def test_segment_coo_batched_index_and_inferred_size(ogn, oracle):
     assert_sum_close(out, gold, scale, torch.float32, "coo batched")
 
 
+def test_segment_coo_index_validation(ogn):
+    # reference csrc/npu/segment_coo/op_host/segment_coo.cpp:97-100
+    src = torch.ones(4, 2, device="cuda")
+    with pytest.raises(RuntimeError, match="non-negative"):
+        ogn.segment_sum_coo(src, torch.tensor([-1, 0, 0, 1], device="cuda"))
+    with pytest.raises(RuntimeError, match="sorted"):
+        ogn.segment_sum_coo(src, torch.tensor([0, 2, 1, 3], device="cuda"))
+    with pytest.raises(RuntimeError, match="exceed"):
+        ogn.segment_sum_coo(src, torch.tensor([0, 1, 2, 3], device="cuda"), dim_size=3)
+    # each row of a batched index is sorted on its own (row ends may drop)
+    s2 = torch.ones(2, 3, device="cuda")
+    got = ogn.segment_sum_coo(s2, torch.tensor([[0, 1, 1], [0, 0, 2]], device="cuda"))
+    assert got.cpu().tolist() == [[1.0, 2.0, 0.0], [2.0, 0.0, 1.0]]
+    with pytest.raises(RuntimeError, match="sorted"):
+        ogn.segment_sum_coo(s2, torch.tensor([[0, 1, 1], [2, 0, 2]], device="cuda"))
+    # the cached facts follow in-place changes of the index
+    idx = torch.tensor([0, 0, 1, 1], device="cuda")
+    ogn.segment_sum_coo(src, idx)
+    idx[1] = 5
+    with pytest.raises(RuntimeError, match="sorted"):
+        ogn.segment_sum_coo(src, idx)
+
+
 # ----------------------------------------------------------------- segment_logsumexp
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("feat", [1, 16, 128])
