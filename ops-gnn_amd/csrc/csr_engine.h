@@ -107,7 +107,7 @@ struct Params {
   float limit;
   int64_t arg_empty;
   float* aux;           // log-sum-exp statistics mode: out <- max, aux <- sum of exp
-  int short_rows;       // contiguous fast variants: chunks of short rows go to short_kernel
+  int short_rows;       // contiguous fast variants: chunks of short rows take short_chunk
 };
 
 template <typename MT>
@@ -236,7 +236,7 @@ __device__ __forceinline__ int64_t chunk_row_end(const Params& p, int64_t pb, in
 
 // A chunk of short rows: on average at most S positions (one step) per row,
 // so that the step schedule would finish a row -- a cross-lane combine --
-// about every step.  Such chunks run on short_kernel instead.
+// about every step.  Such chunks run short_chunk instead.
 __device__ __forceinline__ bool chunk_is_short(int64_t r0, int64_t r_end, int64_t lo, int64_t hi, int S) {
   return (r_end - r0) * S >= hi - lo;
 }
@@ -260,6 +260,110 @@ constexpr int engine_waves() {
   // one 16-byte row per lane: 8 staged positions per lane per window
   if constexpr (G == 1 && VL) return 3;
   return DT != OGN_F32 && RK != RK_SUM ? 3 : 4;
+}
+
+// Chunks of short rows (contiguous mode, fast variants; see chunk_is_short),
+// run by engine_kernel's wave for chunk c instead of the step schedule: the
+// chunk's rows are dealt to the S sub-groups in turn, each sub-group folds
+// its row's positions (four loads in flight) on its own -- no cross-lane
+// combine -- and finishes the row, or leaves the same head / tail record as
+// the step schedule for a row that crosses the chunk's edge.
+template <int DT, int G, bool VL, int RK, int VAR>
+__device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t lo, int64_t hi, int64_t r0,
+                                            int64_t r_end) {
+  using E = Elem<DT>;
+  using S_t = typename E::S;
+  constexpr int NE = VL ? E::VEC : 1;
+  constexpr int S = kWave / G;
+  constexpr int kU = 4;
+  const int lane = lane_id();
+  const int sub = lane / G;
+  const int gl = lane % G;
+  const int64_t b = blockIdx.z;
+  const int64_t pb = p.ptr_bstride ? b : 0;
+  const int64_t K = p.k;
+  const int64_t M = p.m;
+  const int64_t k0 = (int64_t)blockIdx.y * (G * NE) + gl * NE;
+  const bool kok = VL || k0 < K;
+  const int64_t* __restrict__ ptr = static_cast<const int64_t*>(p.ptr) + pb * p.ptr_bstride;
+  const S_t* __restrict__ srcb = static_cast<const S_t*>(p.src) + b * p.src_bstride;
+  const bool is_min = p.reduce == OGN_REDUCE_MIN;
+  // rows r0 .. r_end - 1 end inside the chunk; r_end (< m) may start inside it
+  const int64_t r_last = std::min<int64_t>(r_end, M - 1);
+  for (int64_t r = r0 + sub; r <= r_last; r += S) {
+    const int64_t rs = ptr[r], re = ptr[r + 1];
+    if (r == r_end && rs >= hi) break;  // starts in the next chunk
+    const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(re, hi);
+    float acc[NE], best[NE];
+    int64_t barg[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      acc[i] = 0.f;
+      best[i] = RK == RK_LSE ? -__builtin_inff() : __builtin_nanf("");  // NaN: nothing taken yet
+      barg[i] = kNone;
+    }
+    for (int64_t e0 = a; e0 < z; e0 += kU) {
+      float x[kU][NE];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const bool ok = e0 + u < z && kok;
+        if constexpr (VL) {
+          E::unpack(ok ? load16(srcb + (e0 + u) * K + k0) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+        } else {
+          x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + k0) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        if (e0 + u >= z) break;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+          const float pv = x[u][i];
+          if constexpr (RK == RK_MINMAX) {
+            const bool blocked = VAR == V_LATER ? (is_min ? pv > best[i] : pv < best[i])
+                                                : (is_min ? pv >= best[i] : pv <= best[i]);
+            const bool take = !(pv != pv) && !blocked;
+            best[i] = take ? pv : best[i];
+            barg[i] = take ? e0 + u : barg[i];
+          } else if constexpr (RK == RK_LSE) {
+            lse_add(best[i], acc[i], pv);
+          } else {
+            acc[i] += pv;
+          }
+        }
+      }
+    }
+    if (!kok) continue;
+    if (re > hi || rs < lo) {
+      // partial row: tail if it goes on past the chunk, else head (it began before)
+      const bool head = re <= hi;
+      const int64_t rb = (b * p.nchunks + c) * K + k0;
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        if constexpr (RK == RK_MINMAX) {
+          static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)best[i];
+          (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i];
+        } else if constexpr (RK == RK_LSE) {
+          static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2(best[i], acc[i]);
+        } else {
+          static_cast<float*>(head ? p.rec_head : p.rec_tail)[rb + i] = acc[i];
+        }
+      }
+    } else {
+      const int64_t off = b * p.out_bstride + r * K + k0;
+      float v[NE];
+      int64_t ag[NE];
+#pragma unroll
+      for (int i = 0; i < NE; ++i) finish_elem<RK, float>(p, b, r, k0 + i, rs, re, acc[i], best[i], barg[i], &v[i], &ag[i]);
+      store_floats<NE, true>(p.out, p.out_dt, off, v);
+      if constexpr (RK == RK_MINMAX) {
+        if (p.arg) {
+#pragma unroll
+          for (int i = 0; i < NE; ++i) p.arg[off + i] = ag[i];
+        }
+      }
+    }
+  }
 }
 
 template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER, int VAR>
@@ -310,7 +414,13 @@ void engine_kernel(Params p) {
   const int64_t hi = base + std::min<int64_t>((c + 1) * p.chunk, end);
   int64_t r = c == 0 ? 0 : std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c], 0), M - 1);
   if constexpr (!GATHER && FAST) {
-    if (p.short_rows && chunk_is_short(r, chunk_row_end(p, pb, c, nce), lo, hi, S)) return;  // short_kernel's
+    if (p.short_rows) {
+      const int64_t r_end = chunk_row_end(p, pb, c, nce);
+      if (chunk_is_short(r, r_end, lo, hi, S)) {
+        short_chunk<DT, G, VL, RK, VAR>(p, c, lo, hi, r, r_end);
+        return;
+      }
+    }
   }
 
   // Pointer window: lane j holds ptr[wb + 1 + j].
@@ -644,122 +754,11 @@ void engine_kernel(Params p) {
   }
 }
 
-// Chunks of short rows (contiguous mode, fast variants; see chunk_is_short):
-// the chunk's rows are dealt to the S sub-groups in turn, each sub-group
-// folds its row's positions (four loads in flight) on its own -- no
-// cross-lane combine -- and finishes the row, or leaves the same head / tail
-// record as engine_kernel for a row that crosses the chunk's edge.
-template <int DT, int G, bool VL, int RK, int VAR>
-__global__ __launch_bounds__(kBlock) void short_kernel(Params p) {
-  using E = Elem<DT>;
-  using S_t = typename E::S;
-  constexpr int NE = VL ? E::VEC : 1;
-  constexpr int S = kWave / G;
-  constexpr int kU = 4;
-  const int lane = lane_id();
-  const int sub = lane / G;
-  const int gl = lane % G;
-  const int64_t c = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (c >= p.nchunks) return;
-  const int64_t b = blockIdx.z;
-  const int64_t pb = p.ptr_bstride ? b : 0;
-  const int64_t K = p.k;
-  const int64_t M = p.m;
-  const int64_t k0 = (int64_t)blockIdx.y * (G * NE) + gl * NE;
-  const bool kok = VL || k0 < K;
-  const int64_t* __restrict__ ptr = static_cast<const int64_t*>(p.ptr) + pb * p.ptr_bstride;
-  const S_t* __restrict__ srcb = static_cast<const S_t*>(p.src) + b * p.src_bstride;
-  const bool is_min = p.reduce == OGN_REDUCE_MIN;
-  const int64_t base = ptr[0];
-  const int64_t end = std::max<int64_t>(std::min<int64_t>(ptr[M] - base, p.nnz_bound), 0);
-  const int64_t nce = std::max<int64_t>(1, (end + p.chunk - 1) / p.chunk);
-  if (c >= nce) return;
-  const int64_t lo = base + c * p.chunk;
-  const int64_t hi = base + std::min<int64_t>((c + 1) * p.chunk, end);
-  const int64_t r0 = c == 0 ? 0 : std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c], 0), M - 1);
-  const int64_t r_end = chunk_row_end(p, pb, c, nce);
-  if (!chunk_is_short(r0, r_end, lo, hi, S)) return;
-  // rows r0 .. r_end - 1 end inside the chunk; r_end (< m) may start inside it
-  const int64_t r_last = std::min<int64_t>(r_end, M - 1);
-  for (int64_t r = r0 + sub; r <= r_last; r += S) {
-    const int64_t rs = ptr[r], re = ptr[r + 1];
-    if (r == r_end && rs >= hi) break;  // starts in the next chunk
-    const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(re, hi);
-    float acc[NE], best[NE];
-    int64_t barg[NE];
-#pragma unroll
-    for (int i = 0; i < NE; ++i) {
-      acc[i] = 0.f;
-      best[i] = RK == RK_LSE ? -__builtin_inff() : __builtin_nanf("");  // NaN: nothing taken yet
-      barg[i] = kNone;
-    }
-    for (int64_t e0 = a; e0 < z; e0 += kU) {
-      float x[kU][NE];
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const bool ok = e0 + u < z && kok;
-        if constexpr (VL) {
-          E::unpack(ok ? load16(srcb + (e0 + u) * K + k0) : make_uint4(0u, 0u, 0u, 0u), x[u]);
-        } else {
-          x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + k0) : 0.f;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        if (e0 + u >= z) break;
-#pragma unroll
-        for (int i = 0; i < NE; ++i) {
-          const float pv = x[u][i];
-          if constexpr (RK == RK_MINMAX) {
-            const bool blocked = VAR == V_LATER ? (is_min ? pv > best[i] : pv < best[i])
-                                                : (is_min ? pv >= best[i] : pv <= best[i]);
-            const bool take = !(pv != pv) && !blocked;
-            best[i] = take ? pv : best[i];
-            barg[i] = take ? e0 + u : barg[i];
-          } else if constexpr (RK == RK_LSE) {
-            lse_add(best[i], acc[i], pv);
-          } else {
-            acc[i] += pv;
-          }
-        }
-      }
-    }
-    if (!kok) continue;
-    if (re > hi || rs < lo) {
-      // partial row: tail if it goes on past the chunk, else head (it began before)
-      const bool head = re <= hi;
-      const int64_t rb = (b * p.nchunks + c) * K + k0;
-#pragma unroll
-      for (int i = 0; i < NE; ++i) {
-        if constexpr (RK == RK_MINMAX) {
-          static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)best[i];
-          (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i];
-        } else if constexpr (RK == RK_LSE) {
-          static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2(best[i], acc[i]);
-        } else {
-          static_cast<float*>(head ? p.rec_head : p.rec_tail)[rb + i] = acc[i];
-        }
-      }
-    } else {
-      const int64_t off = b * p.out_bstride + r * K + k0;
-      float v[NE];
-      int64_t ag[NE];
-#pragma unroll
-      for (int i = 0; i < NE; ++i) finish_elem<RK, float>(p, b, r, k0 + i, rs, re, acc[i], best[i], barg[i], &v[i], &ag[i]);
-      store_floats<NE, true>(p.out, p.out_dt, off, v);
-      if constexpr (RK == RK_MINMAX) {
-        if (p.arg) {
-#pragma unroll
-          for (int i = 0; i < NE; ++i) p.arg[off + i] = ag[i];
-        }
-      }
-    }
-  }
-}
-
 // Finish rows that cross chunk boundaries: one wave per chunk that holds the
-// first piece of such a row.  The wave's lanes split into NG = 64 / KW lane
-// groups (KW = K rounded up to a power of two, at most 64); group g folds
+// first piece of such a row.  With K > 32 every lane takes a feature and
+// folds the row's records in chunk order (8 loads in flight).  With K <= 32
+// the wave's lanes split into NG = 64 / KW lane groups (KW = K rounded up to
+// a power of two); group g folds
 // the row's records c + 1 + g, c + 1 + g + NG, ... (8 loads in flight), and
 // the group partials are merged in a butterfly -- so a hub row spread over
 // hundreds of chunks is folded by every lane of the wave, not only by the K
@@ -814,6 +813,84 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   const bool later = p.mm_mode == MM_LATER;
   const bool nanprop = p.mm_mode == MM_NANPROP;
   constexpr int kBatch = 8;
+  if (K > kWave / 2) {
+    // every lane on a feature: one fold in chunk order
+    for (int64_t k = lane; k < K; k += kWave) {
+      const int64_t base_rec = (b * p.nchunks) * K + k;
+      AT a = 0;
+      MT best = 0;
+      int64_t barg = kNone;
+      if constexpr (RK == RK_MINMAX) {
+        best = (MT)static_cast<const double*>(p.rec_tail)[base_rec + c * K];
+        barg = p.arg_tail[base_rec + c * K];
+      } else if constexpr (RK == RK_LSE) {
+        const float2 t = static_cast<const float2*>(p.rec_tail)[base_rec + c * K];
+        best = t.x;
+        a = t.y;
+      } else {
+        a = static_cast<const AT*>(p.rec_tail)[base_rec + c * K];
+      }
+      for (int64_t c0 = c + 1; c0 <= c2; c0 += kBatch) {
+        AT va[kBatch];
+        float vb[kBatch];
+        double vd[kBatch];
+        int64_t vg[kBatch];
+  #pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int64_t cc = c0 + j;
+          const bool ok = cc <= c2;
+          const int64_t ri = base_rec + std::min<int64_t>(cc, c2) * K;
+          const bool head = cc >= c2;
+          if constexpr (RK == RK_MINMAX) {
+            vd[j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
+            vg[j] = ok ? (head ? p.arg_head : p.arg_tail)[ri] : kNone;
+          } else if constexpr (RK == RK_LSE) {
+            const float2 t = ok ? static_cast<const float2*>(head ? p.rec_head : p.rec_tail)[ri]
+                                : make_float2(-__builtin_inff(), 0.f);
+            va[j] = t.x;
+            vb[j] = t.y;
+          } else {
+            va[j] = ok ? static_cast<const AT*>(head ? p.rec_head : p.rec_tail)[ri] : (is_prod ? (AT)1 : (AT)0);
+          }
+        }
+  #pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          if constexpr (RK == RK_MINMAX) {
+            const MT ob = (MT)vd[j];
+            const int64_t oa = vg[j];
+            // later records hold later positions
+            if (oa != kNone && !(nanprop && best != best) &&
+                (barg == kNone || better(ob, best, is_min) || (later && ob == best) || (nanprop && ob != ob))) {
+              best = ob;
+              barg = oa;
+            }
+          } else if constexpr (RK == RK_LSE) {
+            float m = (float)best;
+            float sa = (float)a;
+            lse_merge(m, sa, (float)va[j], vb[j]);
+            best = m;
+            a = (AT)sa;
+          } else {
+            a = is_prod ? a * va[j] : a + va[j];
+          }
+        }
+      }
+      const int64_t off = b * p.out_bstride + r * K + k;
+      if constexpr (INT && RK == RK_SUM) {
+        const int32_t cnt = (int32_t)(re - rs);
+        static_cast<int32_t*>(p.out)[off] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? a / cnt : 0) : a;
+        continue;
+      }
+      float v;
+      int64_t ag = 0;
+      finish_elem<RK, MT>(p, b, r, k, rs, re, (float)a, best, barg, &v, &ag);
+      store_floats<1>(p.out, p.out_dt, off, &v);
+      if constexpr (RK == RK_MINMAX) {
+        if (p.arg) p.arg[off] = ag;
+      }
+    }
+    return;
+  }
   int kw = 1;
   while (kw < K && kw < kWave) kw <<= 1;
   const int ng = kWave / kw;
@@ -836,44 +913,52 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
         a = static_cast<const AT*>(p.rec_tail)[base_rec + c * K];
       }
     }
-    for (int64_t c0 = c + 1 + g; c0 <= c2; c0 += (int64_t)kBatch * ng) {
-      AT va[kBatch];
-      float vb[kBatch];
-      double vd[kBatch];
-      int64_t vg[kBatch];
+    // fold records c0, c0 + ng, ... (B loads in flight per lane; full: only
+    // whole batches; returns where it stopped)
+    auto fold = [&](auto bc, int64_t from, int64_t to, bool full) -> int64_t {
+      constexpr int B = decltype(bc)::value;
+      int64_t c0 = from;
+      for (; full ? c0 + (int64_t)(B - 1) * ng <= to : c0 <= to; c0 += (int64_t)B * ng) {
+        AT va[B];
+        float vb[B];
+        double vd[B];
+        int64_t vg[B];
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int64_t cc = c0 + (int64_t)j * ng;
-        const bool ok = cc <= c2;
-        const int64_t ri = base_rec + std::min<int64_t>(cc, c2) * K;
-        const bool head = cc >= c2;
-        if constexpr (RK == RK_MINMAX) {
-          vd[j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
-          vg[j] = ok ? (head ? p.arg_head : p.arg_tail)[ri] : kNone;
-        } else if constexpr (RK == RK_LSE) {
-          const float2 t = ok ? static_cast<const float2*>(head ? p.rec_head : p.rec_tail)[ri]
-                              : make_float2(-__builtin_inff(), 0.f);
-          va[j] = t.x;
-          vb[j] = t.y;
-        } else {
-          va[j] = ok ? static_cast<const AT*>(head ? p.rec_head : p.rec_tail)[ri] : (is_prod ? (AT)1 : (AT)0);
+        for (int j = 0; j < B; ++j) {
+          const int64_t cc = c0 + (int64_t)j * ng;
+          const bool ok = cc <= to;
+          const int64_t ri = base_rec + std::min<int64_t>(cc, c2) * K;
+          const bool head = cc >= c2;
+          if constexpr (RK == RK_MINMAX) {
+            vd[j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
+            vg[j] = ok ? (head ? p.arg_head : p.arg_tail)[ri] : kNone;
+          } else if constexpr (RK == RK_LSE) {
+            const float2 t = ok ? static_cast<const float2*>(head ? p.rec_head : p.rec_tail)[ri]
+                                : make_float2(-__builtin_inff(), 0.f);
+            va[j] = t.x;
+            vb[j] = t.y;
+          } else {
+            va[j] = ok ? static_cast<const AT*>(head ? p.rec_head : p.rec_tail)[ri] : (is_prod ? (AT)1 : (AT)0);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+          if constexpr (RK == RK_MINMAX) {
+            mm_merge<MT>(best, barg, (MT)vd[j], vg[j], is_min, later, nanprop);
+          } else if constexpr (RK == RK_LSE) {
+            float m = (float)best;
+            float sa = (float)a;
+            lse_merge(m, sa, (float)va[j], vb[j]);
+            best = m;
+            a = (AT)sa;
+          } else {
+            a = is_prod ? a * va[j] : a + va[j];
+          }
         }
       }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        if constexpr (RK == RK_MINMAX) {
-          mm_merge<MT>(best, barg, (MT)vd[j], vg[j], is_min, later, nanprop);
-        } else if constexpr (RK == RK_LSE) {
-          float m = (float)best;
-          float sa = (float)a;
-          lse_merge(m, sa, (float)va[j], vb[j]);
-          best = m;
-          a = (AT)sa;
-        } else {
-          a = is_prod ? a * va[j] : a + va[j];
-        }
-      }
-    }
+      return c0;
+    };
+    fold(std::integral_constant<int, 8>{}, c + 1 + g, c2, false);
     // merge the lane groups (partners kw, 2kw, ... lanes apart)
     for (int d = kw; d < kWave; d <<= 1) {
       if constexpr (RK == RK_MINMAX) {
@@ -941,9 +1026,6 @@ OGN_ENGINE_DECL(launch_contig_f32)
 OGN_ENGINE_DECL(launch_contig_f16)
 OGN_ENGINE_DECL(launch_contig_bf16)
 OGN_ENGINE_DECL(launch_gather_i8)
-OGN_ENGINE_DECL(launch_short_f32)
-OGN_ENGINE_DECL(launch_short_f16)
-OGN_ENGINE_DECL(launch_short_bf16)
 #undef OGN_ENGINE_DECL
 
 template <int DT, typename IDX, bool VL, int RK, bool GATHER, int VAR>
@@ -1011,40 +1093,6 @@ void launch_gather_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s
   } else {
     i64 ? launch_rk<DT, int64_t, RK_SUM, true>(pl, grid, s, p)
         : launch_rk<DT, int32_t, RK_SUM, true>(pl, grid, s, p);
-  }
-}
-
-template <int DT, bool VL, int RK, int VAR>
-void launch_short_g(int g, dim3 grid, hipStream_t s, const Params& p) {
-  switch (g) {
-#define OGN_G(GV) \
-  case GV: hipLaunchKernelGGL((short_kernel<DT, GV, VL, RK, VAR>), grid, dim3(kBlock), 0, s, p); break;
-    OGN_G(1) OGN_G(2) OGN_G(4) OGN_G(8) OGN_G(16) OGN_G(32) OGN_G(64)
-#undef OGN_G
-    default: break;
-  }
-}
-
-template <int DT, int RK, int VAR>
-void launch_short_v(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
-  if (pl.vec) launch_short_g<DT, true, RK, VAR>(pl.g, grid, s, p);
-  else if (pl.g == 1) hipLaunchKernelGGL((short_kernel<DT, 1, false, RK, VAR>), grid, dim3(kBlock), 0, s, p);
-  else hipLaunchKernelGGL((short_kernel<DT, 64, false, RK, VAR>), grid, dim3(kBlock), 0, s, p);
-}
-
-// The short-row pass of contiguous mode (fast variants only; run() sets
-// p.short_rows only for those).
-template <int DT>
-void launch_short_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
-  (void)i64;
-  const int v = variant_of(rk, false, p);
-  if (rk == RK_MINMAX) {
-    if (v == V_LATER) launch_short_v<DT, RK_MINMAX, V_LATER>(pl, grid, s, p);
-    else launch_short_v<DT, RK_MINMAX, V_FIRST>(pl, grid, s, p);
-  } else if (rk == RK_LSE) {
-    launch_short_v<DT, RK_LSE, V_FIRST>(pl, grid, s, p);
-  } else {
-    launch_short_v<DT, RK_SUM, V_FIRST>(pl, grid, s, p);
   }
 }
 

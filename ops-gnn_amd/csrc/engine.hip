@@ -83,7 +83,7 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
   p.nchunks = pl.nchunks;
   const bool i64 = index_dtype == OGN_I64;
   const std::string n(name);
-  // contiguous mode, fast variants: chunks of short rows take short_kernel
+  // contiguous mode, fast variants: chunks of short rows take short_chunk
   p.short_rows = !gather && in_dtype != OGN_I8 && variant_of(rk, false, p) != V_GENERIC &&
                  !std::getenv("OGN_ENGINE_NO_SHORT");
   {
@@ -110,12 +110,6 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
         gather ? launch_gather_bf16(pl, rk, i64, grid, s, p) : launch_contig_bf16(pl, rk, i64, grid, s, p);
         break;
     }
-  }
-  if (p.short_rows) {
-    TimedLaunch t((n + "_short").c_str(), s);
-    if (in_dtype == OGN_F32) launch_short_f32(pl, rk, i64, grid, s, p);
-    else if (in_dtype == OGN_F16) launch_short_f16(pl, rk, i64, grid, s, p);
-    else launch_short_bf16(pl, rk, i64, grid, s, p);
   }
   if (pl.nchunks > 1) {
     TimedLaunch t((n + "_fixup").c_str(), s);

@@ -8,9 +8,5 @@ void launch_contig_bf16(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t
   launch_contig_dt<OGN_BF16>(pl, rk, i64, grid, s, p);
 }
 
-void launch_short_bf16(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
-  launch_short_dt<OGN_BF16>(pl, rk, i64, grid, s, p);
-}
-
 }  // namespace eng
 }  // namespace ogn
