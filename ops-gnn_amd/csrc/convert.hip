@@ -5,9 +5,11 @@
 // search; the top levels of every search hit the same cache lines, so the
 // kernel reads far less than the whole index when rows << numel.
 //
-// ptr2ind: out[e] = r with ptr[r] <= e < ptr[r+1].  Each thread owns 8
-// consecutive edges: one upper_bound search for the first, then a forward
-// walk over rowptr; the 8 results leave as two 32-byte stores.
+// ptr2ind: out[e] = r with ptr[r] <= e < ptr[r+1].  A block owns 2048
+// consecutive edges and stages the pointer entries they can touch in LDS;
+// each thread owns 8 edges: one search in LDS for the first, then a forward
+// walk; the tile's results are transposed through LDS and leave as
+// coalesced 4 KiB store instructions.
 #include "ogn_device.h"
 
 #include <algorithm>
@@ -51,32 +53,125 @@ __global__ __launch_bounds__(256) void ind2ptr_kernel(const IDX* __restrict__ in
   out[i] = lower_bound_idx(ind, numel, i);
 }
 
+// Upper bound of `key` in ptr[0 .. n) for two keys at once: lanes 0-31 search
+// key_lo, lanes 32-63 key_hi.  Each round probes 32 evenly spaced entries
+// and keeps the bracket between the last probe <= key and the first > key,
+// so 10^6 rows take 4 rounds of one load each (instead of 20 dependent
+// loads of a per-thread binary search).  Called by the whole wavefront.
 template <typename IDX>
-__global__ __launch_bounds__(256) void ptr2ind_kernel(const IDX* __restrict__ ptr, int64_t rows,
-                                                      int64_t numel, int64_t* __restrict__ out) {
-  const int64_t e0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kEdgesPerThread;
-  if (e0 >= numel) return;
-  // Row of edge e0: the last r with ptr[r] <= e0 (rows with ptr[r] == ptr[r+1]
-  // are skipped because the search lands on the last equal pointer).
-  int64_t r = upper_bound_idx(ptr, rows + 1, e0) - 1;
-  r = std::min<int64_t>(std::max<int64_t>(r, 0), std::max<int64_t>(rows - 1, 0));
-  int64_t next = ptr[r + 1];
-  int64_t res[kEdgesPerThread];
-#pragma unroll
-  for (int i = 0; i < kEdgesPerThread; ++i) {
-    const int64_t e = e0 + i;
-    while (e >= next && r + 1 < rows) {
-      ++r;
-      next = ptr[r + 1];
+__device__ __forceinline__ int64_t wave_upper_bound2(const IDX* __restrict__ ptr, int64_t n, int64_t key_lo,
+                                                     int64_t key_hi) {
+  const int lane = lane_id();
+  const int half = lane >> 5, j = lane & 31;
+  const int64_t key = half ? key_hi : key_lo;
+  int64_t lo = 0, hi = n;
+  while (true) {
+    const bool done = lo >= hi;
+    if (__all(done)) break;
+    const int64_t step = done ? 1 : (hi - lo + 31) / 32;
+    const int64_t q = lo + (int64_t)j * step;
+    const bool valid = !done && q < hi;
+    const bool le = valid && (int64_t)ptr[q] <= key;
+    const uint64_t m = __ballot(le);
+    const uint64_t mv = __ballot(valid);
+    const uint32_t mh = (uint32_t)(half ? (m >> 32) : m);
+    const uint32_t vh = (uint32_t)(half ? (mv >> 32) : mv);
+    const int c = __popc(mh);  // probes <= key form a prefix of the valid ones
+    const int nv = __popc(vh);
+    if (!done) {
+      const int64_t nlo = c > 0 ? lo + (int64_t)(c - 1) * step + 1 : lo;
+      const int64_t nhi = c < nv ? lo + (int64_t)c * step : hi;
+      lo = nlo;
+      hi = c > 0 ? nhi : lo;
     }
-    res[i] = r;
   }
-  if (e0 + kEdgesPerThread <= numel) {
-    longlong2* o = reinterpret_cast<longlong2*>(out + e0);
-#pragma unroll
-    for (int i = 0; i < kEdgesPerThread / 2; ++i) o[i] = make_longlong2(res[2 * i], res[2 * i + 1]);
+  return lo;
+}
+
+constexpr int kTileThreads = 256;
+constexpr int64_t kTileEdges = (int64_t)kTileThreads * kEdgesPerThread;
+constexpr int kWindow = 2176;  // pointer entries staged in LDS per tile (17 KiB: 9 blocks per CU)
+
+// A block owns a tile of 2048 edges.  Its first wavefront finds the rows of
+// the tile's first and last edges; the pointer entries between them (the
+// only rows the tile can touch) go to LDS, and every thread finds the row of
+// its first edge by binary search in LDS, then walks its 8 edges.  A tile
+// that spans more than kWindow pointer entries (long runs of empty rows)
+// searches global memory instead.
+template <typename IDX>
+__global__ __launch_bounds__(kTileThreads) void ptr2ind_kernel(const IDX* __restrict__ ptr, int64_t rows,
+                                                              int64_t numel, int64_t* __restrict__ out) {
+  __shared__ int64_t win[kWindow];
+  __shared__ int64_t bounds[2];
+  const int64_t t0 = (int64_t)blockIdx.x * kTileEdges;
+  const int64_t t1 = std::min<int64_t>(t0 + kTileEdges, numel) - 1;
+  if (threadIdx.x < kWave) {
+    const int64_t ub = wave_upper_bound2(ptr, rows + 1, t0, t1);
+    if (threadIdx.x == 0) bounds[0] = ub;
+    if (threadIdx.x == 32) bounds[1] = ub;
+  }
+  __syncthreads();
+  const int64_t last = std::max<int64_t>(rows - 1, 0);
+  const int64_t r_lo = std::min<int64_t>(std::max<int64_t>(bounds[0] - 1, 0), last);
+  const int64_t r_hi = std::min<int64_t>(std::max<int64_t>(bounds[1] - 1, 0), last);
+  const int64_t nwin = r_hi - r_lo + 2;  // ptr[r_lo .. r_hi + 1]
+  const bool staged = nwin <= kWindow;
+  if (staged) {
+    for (int64_t i = threadIdx.x; i < nwin; i += kTileThreads) win[i] = (int64_t)ptr[r_lo + i];
+  }
+  __syncthreads();
+  const int64_t e0 = t0 + (int64_t)threadIdx.x * kEdgesPerThread;
+  int64_t r = 0;
+  if (e0 >= numel) {
+    // no edges: nothing to find (the thread still joins the barrier below)
+  } else if (staged) {
+    // last window entry <= e0 (entry 0 holds ptr[r_lo] <= t0 <= e0, unless e0
+    // precedes every row start: then row r_lo, as the clamp above gives)
+    int64_t lo = 0, len = nwin;
+    while (len > 0) {
+      const int64_t h = len >> 1;
+      const bool right = win[lo + h] <= e0;
+      lo = right ? lo + h + 1 : lo;
+      len = right ? len - h - 1 : h;
+    }
+    r = std::min<int64_t>(std::max<int64_t>(r_lo + lo - 1, 0), last);
   } else {
-    for (int i = 0; i < kEdgesPerThread && e0 + i < numel; ++i) out[e0 + i] = res[i];
+    r = std::min<int64_t>(std::max<int64_t>(upper_bound_idx(ptr, rows + 1, e0) - 1, 0), last);
+  }
+  const auto ptr_at = [&](int64_t i) -> int64_t {
+    return staged && i - r_lo < nwin ? win[i - r_lo] : (int64_t)ptr[i];
+  };
+  int64_t res[kEdgesPerThread];
+  if (e0 < numel) {
+    int64_t next = ptr_at(r + 1);
+#pragma unroll
+    for (int i = 0; i < kEdgesPerThread; ++i) {
+      const int64_t e = e0 + i;
+      while (e >= next && r + 1 < rows) {
+        ++r;
+        next = ptr_at(r + 1);
+      }
+      res[i] = r;
+    }
+  }
+  // Transpose through LDS (reusing the window) so that every store
+  // instruction writes 256 consecutive 16-byte pieces (4 KiB) of the tile.
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kEdgesPerThread; ++i) win[threadIdx.x * kEdgesPerThread + i] = res[i];
+  __syncthreads();
+  const int64_t n_tile = t1 - t0 + 1;
+  typedef long long v2i64 __attribute__((ext_vector_type(2)));
+  const v2i64* w2 = reinterpret_cast<const v2i64*>(win);
+  if (n_tile == kTileEdges) {
+    v2i64* o = reinterpret_cast<v2i64*>(out + t0);
+#pragma unroll
+    for (int k = 0; k < kEdgesPerThread / 2; ++k) {
+      const int q = k * kTileThreads + threadIdx.x;
+      __builtin_nontemporal_store(w2[q], &o[q]);
+    }
+  } else {
+    for (int64_t q = threadIdx.x; q < n_tile; q += kTileThreads) out[t0 + q] = win[q];
   }
 }
 
@@ -116,8 +211,7 @@ int ogn_ptr2ind(const void* ptr, int index_dtype, int64_t rows, int64_t numel, i
   if ((uintptr_t)out % 16 != 0) return fail(OGN_EINVAL, "ogn_ptr2ind: out must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   TimedLaunch t("ptr2ind", s);
-  const int64_t threads = (numel + kEdgesPerThread - 1) / kEdgesPerThread;
-  const dim3 g((unsigned)((threads + 255) / 256));
+  const dim3 g((unsigned)((numel + kTileEdges - 1) / kTileEdges));
   if (index_dtype == OGN_I64)
     hipLaunchKernelGGL(ptr2ind_kernel<int64_t>, g, dim3(256), 0, s, static_cast<const int64_t*>(ptr),
                        rows, numel, out);

@@ -72,3 +72,16 @@ def test_argument_errors(ogn):
         ogn.ind2ptr(torch.zeros(2, dtype=torch.long, device="cuda"), -1)
     with pytest.raises(RuntimeError, match="at least one"):
         ogn.ptr2ind(torch.zeros(0, dtype=torch.long, device="cuda"), 0)
+
+
+def test_ptr2ind_tiles_with_empty_row_runs(ogn, oracle):
+    # tiles of 2048 edges stage their pointer entries in LDS (up to 2176);
+    # long runs of empty rows inside a tile take the global search instead
+    rng = np.random.default_rng(8)
+    deg = rng.integers(0, 5, 30_000)
+    deg[5000:15000] = 0          # 10 000 empty rows inside one tile
+    deg[20000] = 7000            # a row spanning several tiles
+    ptr = np.concatenate([[0], np.cumsum(deg)])
+    edges = int(ptr[-1])
+    out = ogn.ptr2ind(torch.from_numpy(ptr).cuda(), edges)
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.ptr2ind(ptr, edges))
