@@ -13,6 +13,7 @@
 // with consecutive threads on consecutive packets, so reads of one source
 // row and writes of the tile are coalesced.
 #include "ogn_device.h"
+#include "search.h"
 
 #include <algorithm>
 
@@ -40,25 +41,63 @@ template <> struct Packet<4> { using T = uint32_t; };
 template <> struct Packet<2> { using T = uint16_t; };
 template <> struct Packet<1> { using T = uint8_t; };
 
+// Pointer entries a CSR tile stages in LDS: its 64 rows touch at most 64
+// non-empty segments; longer runs of empty segments search global memory.
+constexpr int kPtrWindow = 128;
+
 template <int P, bool CSR>
 __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
   using T = typename Packet<P>::T;
   __shared__ int64_t rows[kTileRows];
+  __shared__ int64_t win[CSR ? kPtrWindow : 1];
+  __shared__ int64_t bounds[2];
   const int64_t b = blockIdx.y;
   const int64_t i0 = (int64_t)blockIdx.x * kTileRows;
   const int64_t nrows = std::min<int64_t>(kTileRows, a.out_rows - i0);
+  int64_t s_lo = 0, nwin = 0;
+  if constexpr (CSR) {
+    // the segments of the tile's first and last rows (one 32-way search per
+    // wavefront instead of a binary search per row), then their pointer
+    // entries into LDS
+    const int64_t* ptr = a.ptr + b * a.ptr_bstride;
+    if (threadIdx.x < kWave) {
+      const int64_t ub = wave_upper_bound2(ptr, a.src_rows + 1, i0, i0 + nrows - 1);
+      if (threadIdx.x == 0) bounds[0] = ub;
+      if (threadIdx.x == 32) bounds[1] = ub;
+    }
+    __syncthreads();
+    s_lo = std::max<int64_t>(bounds[0] - 1, 0);
+    nwin = std::min<int64_t>(bounds[1], a.src_rows + 1) - s_lo;  // ptr[s_lo .. ub(last) - 1]
+    if (nwin <= kPtrWindow && threadIdx.x < nwin) win[threadIdx.x] = ptr[s_lo + threadIdx.x];
+    __syncthreads();
+  }
   if (threadIdx.x < nrows) {
     const int64_t i = i0 + threadIdx.x;
     int64_t s;
     if constexpr (CSR) {
       // last s with ptr[s] <= i (segments = src_rows); -1 before ptr[0]
-      const int64_t* ptr = a.ptr + b * a.ptr_bstride;
-      int64_t lo = 0, n = a.src_rows + 1;  // search ptr[0 .. segments]
-      while (n > 0) {
-        const int64_t half = n >> 1;
-        const bool right = ptr[lo + half] <= i;
-        lo = right ? lo + half + 1 : lo;
-        n = right ? n - half - 1 : half;
+      int64_t lo, n;
+      if (nwin <= kPtrWindow) {
+        // every entry of ptr before s_lo is <= i, every entry past the window > i
+        lo = 0;
+        n = nwin;
+        while (n > 0) {
+          const int64_t half = n >> 1;
+          const bool right = win[lo + half] <= i;
+          lo = right ? lo + half + 1 : lo;
+          n = right ? n - half - 1 : half;
+        }
+        lo += s_lo;
+      } else {
+        const int64_t* ptr = a.ptr + b * a.ptr_bstride;
+        lo = 0;
+        n = a.src_rows + 1;  // search ptr[0 .. segments]
+        while (n > 0) {
+          const int64_t half = n >> 1;
+          const bool right = ptr[lo + half] <= i;
+          lo = right ? lo + half + 1 : lo;
+          n = right ? n - half - 1 : half;
+        }
       }
       s = lo - 1;  // number of entries <= i, minus one
       if (s >= a.src_rows) s = -1;  // past the last segment end (not produced)

@@ -193,3 +193,12 @@ def test_empty_shapes(ogn):
     assert out.shape == (3, 0)
     out = ogn.gather_coo(torch.randn(3, 4, device="cuda"), torch.empty(0, dtype=torch.int64, device="cuda"))
     assert out.shape == (0, 4)
+
+
+def test_gather_csr_long_empty_segment_runs(ogn, oracle):
+    # a 64-row tile stages up to 128 pointer entries in LDS; a run of 5000
+    # empty segments inside one tile takes the global search instead
+    lengths = np.array([3] * 40 + [0] * 5000 + [7] * 30 + [0] * 200 + [1] * 500)
+    ptr = np.concatenate([[0], np.cumsum(lengths)])
+    src = _make_src((lengths.size, 6), torch.float32, 5)
+    _assert_bitwise(ogn.gather_csr(src.cuda(), torch.from_numpy(ptr).cuda()), oracle.gather_csr(src, ptr))
