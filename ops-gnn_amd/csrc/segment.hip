@@ -69,8 +69,9 @@ __global__ __launch_bounds__(256) void index_facts_kernel(const int64_t* __restr
 // One-feature rows (k == 1) that are long on average: one wavefront per
 // (batch, row).  Lanes read the row as aligned 16-byte packets (8 fp16/bf16
 // or 4 fp32 positions), fold each packet into the log-sum-exp state (m, s)
-// with one rescale, and merge the 64 lane states in a butterfly (fmax and +
-// commute, so every lane ends with the same bits).  The general engine
+// with one rescale, and combine the 64 lane states with a max butterfly and
+// a sum butterfly (fmax and + commute, so every lane ends with the same
+// bits).  The general engine
 // spreads one-feature rows over 64 lanes with one 2-byte load each; here
 // every load is a full packet, and only the two packets a row shares with
 // its neighbours pay for per-position masks.
@@ -108,17 +109,25 @@ __device__ __forceinline__ void row_lse_k1(const typename Elem<DT>::S* row, int6
     m = pm;
     sacc = t;
   }
-  auto merge = [&](auto offc) {
-    constexpr int off = decltype(offc)::value;
-    const float om = xor_shfl<off>(m), os = xor_shfl<off>(sacc);
-    lse_merge(m, sacc, om, os);
-  };
-  merge(std::integral_constant<int, 1>{});
-  merge(std::integral_constant<int, 2>{});
-  merge(std::integral_constant<int, 4>{});
-  merge(std::integral_constant<int, 8>{});
-  merge(std::integral_constant<int, 16>{});
-  merge(std::integral_constant<int, 32>{});
+  // Across the 64 lanes: the row maximum first (a max butterfly), then each
+  // lane rescales its sum to that maximum once and a sum butterfly adds
+  // them -- two cheap butterflies instead of six log-sum-exp merges.
+  float gm = m;
+  gm = fmaxf(gm, xor_shfl<1>(gm));
+  gm = fmaxf(gm, xor_shfl<2>(gm));
+  gm = fmaxf(gm, xor_shfl<4>(gm));
+  gm = fmaxf(gm, xor_shfl<8>(gm));
+  gm = fmaxf(gm, xor_shfl<16>(gm));
+  gm = fmaxf(gm, xor_shfl<32>(gm));
+  float sv = sacc == 0.f ? 0.f : sacc * fast_exp(clampf_max(m) - clampf_max(gm));
+  sv += xor_shfl<1>(sv);
+  sv += xor_shfl<2>(sv);
+  sv += xor_shfl<4>(sv);
+  sv += xor_shfl<8>(sv);
+  sv += xor_shfl<16>(sv);
+  sv += xor_shfl<32>(sv);
+  m = gm;
+  sacc = sv;
 }
 
 // 4 wavefronts per block, one row each.
