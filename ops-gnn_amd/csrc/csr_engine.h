@@ -1003,7 +1003,8 @@ struct Plan {
   int64_t nchunks;
 };
 
-Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned);
+// gather: SpMM (feature rows gathered through col) rather than contiguous rows.
+Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned, bool gather = false);
 
 struct Workspace {
   size_t chunk_row, head, tail, arg_head, arg_tail, total;

@@ -8,7 +8,7 @@
 namespace ogn {
 namespace eng {
 
-Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned) {
+Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned, bool gather) {
   Plan pl{};
   const int esz = dtype_size(in_dtype);
   const int vec = 16 / esz;
@@ -30,9 +30,19 @@ Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned) {
     pl.g = 64;
     pl.tiles = (k + 63) / 64;
   }
-  // About 128 KiB of feature traffic per wave, in whole 64-position windows.
+  // Feature traffic per wave, in whole 64-position windows: 128 KiB in
+  // contiguous mode (short rows: more, shorter chunks keep the tail small),
+  // 256 KiB in gather mode, where halving the chunk count halves the rows
+  // that cross a chunk boundary and so the fix-up pass (config 3 SpMM sum
+  // step 5.79 -> 5.70 ms, max 7.27 -> 6.96 ms; contiguous config 5 scatter
+  // got slower with 256 KiB: 1.49 -> 1.52 ms).
   const int64_t row_bytes = std::max<int64_t>(1, std::min<int64_t>(k, 64 * vec) * esz);
-  int64_t chunk = (131072 / row_bytes + 63) / 64 * 64;
+  int64_t wave_bytes = gather ? 262144 : 131072;
+  if (const char* env = std::getenv("OGN_ENGINE_WAVE_KIB")) {
+    const long v = std::atol(env);
+    if (v >= 16) wave_bytes = (int64_t)v * 1024;
+  }
+  int64_t chunk = (wave_bytes / row_bytes + 63) / 64 * 64;
   if (const char* env = std::getenv("OGN_ENGINE_CHUNK")) {
     const long v = std::atol(env);
     if (v >= 64) chunk = v / 64 * 64;

@@ -17,8 +17,8 @@ size_t ogn_spmm_csr_workspace_size(int64_t m, int64_t nnz, int64_t k, int64_t ba
   (void)m;
   if (nnz < 0 || k <= 0 || batch <= 0) return 0;
   const int rk = (reduce == OGN_REDUCE_MIN || reduce == OGN_REDUCE_MAX) ? RK_MINMAX : RK_SUM;
-  const Plan pa = make_plan(nnz, k, in_dtype, true);
-  const Plan pu = make_plan(nnz, k, in_dtype, false);
+  const Plan pa = make_plan(nnz, k, in_dtype, true, true);
+  const Plan pu = make_plan(nnz, k, in_dtype, false, true);
   return std::max(workspace_layout(pa, k, batch, 1, rk).total, workspace_layout(pu, k, batch, 1, rk).total);
 }
 
@@ -85,7 +85,7 @@ static int spmm_impl(const void* rowptr, const void* col, int index_dtype, const
 
   const bool aligned = is_aligned(mat, 16) && is_aligned(out, 16) &&
                        (!value || value_width == 1 || is_aligned(value, 16));
-  const Plan pl = make_plan(nnz, k, in_dtype, aligned);
+  const Plan pl = make_plan(nnz, k, in_dtype, aligned, true);
   Params p{};
   p.ptr = rowptr;
   p.ptr_bstride = 0;
