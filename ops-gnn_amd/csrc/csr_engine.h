@@ -814,79 +814,106 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   const bool nanprop = p.mm_mode == MM_NANPROP;
   constexpr int kBatch = 8;
   if (K > kWave / 2) {
-    // every lane on a feature: one fold in chunk order
-    for (int64_t k = lane; k < K; k += kWave) {
-      const int64_t base_rec = (b * p.nchunks) * K + k;
-      AT a = 0;
-      MT best = 0;
-      int64_t barg = kNone;
-      if constexpr (RK == RK_MINMAX) {
-        best = (MT)static_cast<const double*>(p.rec_tail)[base_rec + c * K];
-        barg = p.arg_tail[base_rec + c * K];
-      } else if constexpr (RK == RK_LSE) {
-        const float2 t = static_cast<const float2*>(p.rec_tail)[base_rec + c * K];
-        best = t.x;
-        a = t.y;
-      } else {
-        a = static_cast<const AT*>(p.rec_tail)[base_rec + c * K];
+    // every lane on a feature: one fold in chunk order.  A lane folds its
+    // features k and k + 64 together (NF = 2), so the record loads of both
+    // are in flight at once and a wave walks its row's chain of dependent
+    // loads once for K <= 128 instead of once per 64 features.
+    constexpr int NF = 2;
+    for (int64_t k0 = lane; k0 < K; k0 += NF * kWave) {
+      bool fok[NF];
+      int64_t base_rec[NF];
+      AT a[NF];
+      MT best[NF];
+      int64_t barg[NF];
+  #pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int64_t k = k0 + f * kWave;
+        fok[f] = k < K;
+        base_rec[f] = (b * p.nchunks) * K + (fok[f] ? k : k0);
+        a[f] = 0;
+        best[f] = 0;
+        barg[f] = kNone;
+        if constexpr (RK == RK_MINMAX) {
+          best[f] = (MT)static_cast<const double*>(p.rec_tail)[base_rec[f] + c * K];
+          barg[f] = p.arg_tail[base_rec[f] + c * K];
+        } else if constexpr (RK == RK_LSE) {
+          const float2 t = static_cast<const float2*>(p.rec_tail)[base_rec[f] + c * K];
+          best[f] = t.x;
+          a[f] = t.y;
+        } else {
+          a[f] = static_cast<const AT*>(p.rec_tail)[base_rec[f] + c * K];
+        }
       }
       for (int64_t c0 = c + 1; c0 <= c2; c0 += kBatch) {
-        AT va[kBatch];
-        float vb[kBatch];
-        double vd[kBatch];
-        int64_t vg[kBatch];
+        AT va[NF][kBatch];
+        float vb[NF][kBatch];
+        double vd[NF][kBatch];
+        int64_t vg[NF][kBatch];
   #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
           const int64_t cc = c0 + j;
           const bool ok = cc <= c2;
-          const int64_t ri = base_rec + std::min<int64_t>(cc, c2) * K;
           const bool head = cc >= c2;
-          if constexpr (RK == RK_MINMAX) {
-            vd[j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
-            vg[j] = ok ? (head ? p.arg_head : p.arg_tail)[ri] : kNone;
-          } else if constexpr (RK == RK_LSE) {
-            const float2 t = ok ? static_cast<const float2*>(head ? p.rec_head : p.rec_tail)[ri]
-                                : make_float2(-__builtin_inff(), 0.f);
-            va[j] = t.x;
-            vb[j] = t.y;
-          } else {
-            va[j] = ok ? static_cast<const AT*>(head ? p.rec_head : p.rec_tail)[ri] : (is_prod ? (AT)1 : (AT)0);
+  #pragma unroll
+          for (int f = 0; f < NF; ++f) {
+            const int64_t ri = base_rec[f] + std::min<int64_t>(cc, c2) * K;
+            if constexpr (RK == RK_MINMAX) {
+              vd[f][j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
+              vg[f][j] = ok ? (head ? p.arg_head : p.arg_tail)[ri] : kNone;
+            } else if constexpr (RK == RK_LSE) {
+              const float2 t = ok ? static_cast<const float2*>(head ? p.rec_head : p.rec_tail)[ri]
+                                  : make_float2(-__builtin_inff(), 0.f);
+              va[f][j] = t.x;
+              vb[f][j] = t.y;
+            } else {
+              va[f][j] = ok ? static_cast<const AT*>(head ? p.rec_head : p.rec_tail)[ri]
+                            : (is_prod ? (AT)1 : (AT)0);
+            }
           }
         }
   #pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-          if constexpr (RK == RK_MINMAX) {
-            const MT ob = (MT)vd[j];
-            const int64_t oa = vg[j];
-            // later records hold later positions
-            if (oa != kNone && !(nanprop && best != best) &&
-                (barg == kNone || better(ob, best, is_min) || (later && ob == best) || (nanprop && ob != ob))) {
-              best = ob;
-              barg = oa;
+        for (int f = 0; f < NF; ++f) {
+  #pragma unroll
+          for (int j = 0; j < kBatch; ++j) {
+            if constexpr (RK == RK_MINMAX) {
+              const MT ob = (MT)vd[f][j];
+              const int64_t oa = vg[f][j];
+              // later records hold later positions
+              if (oa != kNone && !(nanprop && best[f] != best[f]) &&
+                  (barg[f] == kNone || better(ob, best[f], is_min) || (later && ob == best[f]) ||
+                   (nanprop && ob != ob))) {
+                best[f] = ob;
+                barg[f] = oa;
+              }
+            } else if constexpr (RK == RK_LSE) {
+              float m = (float)best[f];
+              float sa = (float)a[f];
+              lse_merge(m, sa, (float)va[f][j], vb[f][j]);
+              best[f] = m;
+              a[f] = (AT)sa;
+            } else {
+              a[f] = is_prod ? a[f] * va[f][j] : a[f] + va[f][j];
             }
-          } else if constexpr (RK == RK_LSE) {
-            float m = (float)best;
-            float sa = (float)a;
-            lse_merge(m, sa, (float)va[j], vb[j]);
-            best = m;
-            a = (AT)sa;
-          } else {
-            a = is_prod ? a * va[j] : a + va[j];
           }
         }
       }
-      const int64_t off = b * p.out_bstride + r * K + k;
-      if constexpr (INT && RK == RK_SUM) {
-        const int32_t cnt = (int32_t)(re - rs);
-        static_cast<int32_t*>(p.out)[off] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? a / cnt : 0) : a;
-        continue;
-      }
-      float v;
-      int64_t ag = 0;
-      finish_elem<RK, MT>(p, b, r, k, rs, re, (float)a, best, barg, &v, &ag);
-      store_floats<1>(p.out, p.out_dt, off, &v);
-      if constexpr (RK == RK_MINMAX) {
-        if (p.arg) p.arg[off] = ag;
+  #pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        if (!fok[f]) continue;
+        const int64_t k = k0 + f * kWave;
+        const int64_t off = b * p.out_bstride + r * K + k;
+        if constexpr (INT && RK == RK_SUM) {
+          const int32_t cnt = (int32_t)(re - rs);
+          static_cast<int32_t*>(p.out)[off] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? a[f] / cnt : 0) : a[f];
+          continue;
+        }
+        float v;
+        int64_t ag = 0;
+        finish_elem<RK, MT>(p, b, r, k, rs, re, (float)a[f], best[f], barg[f], &v, &ag);
+        store_floats<1>(p.out, p.out_dt, off, &v);
+        if constexpr (RK == RK_MINMAX) {
+          if (p.arg) p.arg[off] = ag;
+        }
       }
     }
     return;

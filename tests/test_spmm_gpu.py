@@ -123,7 +123,7 @@ def _powerlaw(m, n, nnz, cap, seed):
     return torch.from_numpy(ptr), torch.from_numpy(col), rng
 
 
-@pytest.mark.parametrize("k", [1, 4, 8, 17, 32, 64, 128, 200, 256, 512, 1024])
+@pytest.mark.parametrize("k", [1, 4, 8, 17, 32, 40, 64, 96, 128, 200, 256, 512, 1024])
 @pytest.mark.parametrize("reduce", ["sum", "mean", "max"])
 def test_powerlaw_feature_widths(ogn, oracle, k, reduce):
     ptr, col, rng = _powerlaw(3000, 2500, 60_000, 6000, seed=k)
