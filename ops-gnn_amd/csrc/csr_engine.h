@@ -29,6 +29,7 @@
 #pragma once
 
 #include "ogn_device.h"
+#include "search.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -89,6 +90,8 @@ struct Params {
   int64_t out_bstride;  // elements between batches of out
   int64_t* arg;
   int64_t* chunk_row;   // [ptr batches][nchunks]
+  longlong4* fix;       // [ptr batches][nchunks] {r, ptr[r], ptr[r + 1], -} of the
+                        // row crossing chunk c's end from inside c; r = -1: none
   void* rec_head;       // [batch][nchunks][k] partial values
   void* rec_tail;
   int64_t* arg_head;    // [batch][nchunks][k] partial args (min/max)
@@ -210,21 +213,55 @@ __device__ __forceinline__ void finish_elem(const Params& p, int64_t b, int64_t 
   }
 }
 
-// Row ids of the first position of every chunk: row r owns the chunk starts
-// that fall inside [ptr[r], ptr[r+1]).
+// Row ids of the first position of every chunk (chunk_row[c]: the row r
+// with ptr[r] <= base + c * chunk < ptr[r + 1]), and the fix-up entries
+// (fix[c - 1]: that row when it starts inside chunk c - 1, so crosses its
+// end; r = -1 otherwise).  One lane per chunk: the block brackets the rows of
+// its 256 chunk starts with one 32-way wave search, stages that window of
+// ptr in LDS when it holds at most kRowWindow entries, and each lane
+// binary-searches its own start there (in global memory for a wider
+// window).  A hub row spanning thousands of chunks costs no thread more than
+// any other.  Every entry below the chunk count is rewritten on every call.
+constexpr int kRowWindow = 4096;
 template <typename IDX>
 __global__ __launch_bounds__(256) void chunk_rows_kernel(Params p) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= p.m) return;
+  __shared__ int64_t win[kRowWindow];
+  __shared__ int64_t bracket[2];
+  const int64_t cb = (int64_t)blockIdx.x * blockDim.x;  // the block's first chunk
+  const int64_t c = cb + threadIdx.x;
   const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr) + blockIdx.y * p.ptr_bstride;
   const int64_t base = ptr[0];
-  const int64_t a = (int64_t)ptr[r] - base, z = (int64_t)ptr[r + 1] - base;
-  if (z <= a) return;
-  int64_t c0 = (a + p.chunk - 1) / p.chunk, c1 = (z - 1) / p.chunk;
-  c0 = std::max<int64_t>(c0, 0);
-  c1 = std::min<int64_t>(c1, p.nchunks - 1);
-  int64_t* __restrict__ cr = p.chunk_row + blockIdx.y * p.nchunks;
-  for (int64_t c = c0; c <= c1; ++c) cr[c] = r;
+  const int64_t total = std::max<int64_t>((int64_t)ptr[p.m] - base, 0);
+  const int64_t nce = std::min<int64_t>(p.nchunks, (total + p.chunk - 1) / p.chunk);
+  if (cb >= nce) return;  // whole block
+  const int64_t clast = std::min<int64_t>(cb + (int64_t)blockDim.x - 1, nce - 1);
+  if (threadIdx.x < kWave) {
+    const int64_t ub = wave_upper_bound2(ptr, p.m + 1, base + cb * p.chunk, base + clast * p.chunk);
+    if (threadIdx.x == 0 || threadIdx.x == 32) bracket[threadIdx.x >> 5] = ub;
+  }
+  __syncthreads();
+  const int64_t L = bracket[0], H = bracket[1];  // every answer lies in [L, H]
+  const bool staged = H - L <= kRowWindow;
+  if (staged) {
+    for (int64_t i = threadIdx.x; i < H - L; i += blockDim.x) win[i] = ptr[L + i];
+    __syncthreads();
+  }
+  if (c > clast) return;
+  const int64_t key = base + c * p.chunk;
+  int64_t lo = L, hi = H;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    const int64_t v = staged ? win[mid - L] : (int64_t)ptr[mid];
+    if (v <= key) lo = mid + 1;
+    else hi = mid;
+  }
+  const int64_t r = std::min<int64_t>(std::max<int64_t>(lo - 1, 0), p.m - 1);
+  p.chunk_row[blockIdx.y * p.nchunks + c] = r;
+  if (c >= 1) {
+    const int64_t rs = ptr[r], re = ptr[r + 1];
+    const bool crosses = rs >= base + (c - 1) * p.chunk && rs < base + c * p.chunk;
+    p.fix[blockIdx.y * p.nchunks + c - 1] = crosses ? make_longlong4(r, rs, re, 0) : make_longlong4(-1, 0, 0, 0);
+  }
 }
 
 // Chunk c holds rows r0 (the row of its first position) up to r_end, the
@@ -801,11 +838,11 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   const int64_t end = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[p.m] - base, p.nnz_bound), 0);
   const int64_t nce = std::max<int64_t>(1, (end + p.chunk - 1) / p.chunk);
   if (c + 1 >= nce) return;
-  const int64_t lo = base + c * p.chunk, hi = lo + p.chunk;
-  const int64_t r = std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c + 1], 0), p.m - 1);
-  const int64_t rs = ptr[r];
-  if (!(rs < hi && rs >= lo)) return;
-  const int64_t re = ptr[r + 1];
+  // The row that starts inside chunk c and ends past it, from the chunk-row
+  // pass (one load instead of chunk_row -> ptr[r] -> ptr[r + 1]).
+  const longlong4 fx = p.fix[pb * p.nchunks + c];
+  if (fx.x < 0 || fx.x >= p.m) return;
+  const int64_t r = fx.x, rs = fx.y, re = fx.z;
   const int64_t c2 = std::min<int64_t>((re - 1 - base) / p.chunk, nce - 1);
   const int64_t K = p.k;
   const bool is_min = p.reduce == OGN_REDUCE_MIN;
@@ -1034,7 +1071,7 @@ struct Plan {
 Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned, bool gather = false);
 
 struct Workspace {
-  size_t chunk_row, head, tail, arg_head, arg_tail, total;
+  size_t chunk_row, fix, head, tail, arg_head, arg_tail, total;
 };
 
 Workspace workspace_layout(const Plan& pl, int64_t k, int64_t batch, int64_t ptr_batches, int rk);

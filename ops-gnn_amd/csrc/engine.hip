@@ -63,7 +63,8 @@ Workspace workspace_layout(const Plan& pl, int64_t k, int64_t batch, int64_t ptr
   Workspace w{};
   const size_t rec = (size_t)pl.nchunks * batch * k;
   w.chunk_row = 0;
-  w.head = align256(sizeof(int64_t) * pl.nchunks * ptr_batches);
+  w.fix = align256(sizeof(int64_t) * pl.nchunks * ptr_batches);
+  w.head = w.fix + align256(sizeof(longlong4) * pl.nchunks * ptr_batches);
   const size_t vsz = rk == RK_SUM ? sizeof(float) : (rk == RK_LSE ? sizeof(float2) : sizeof(double));
   const size_t vbytes = align256(rec * vsz);
   w.tail = w.head + vbytes;
@@ -85,6 +86,7 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
     return fail(OGN_EUNSUPPORTED, std::string(name) + ": batch or feature tiles exceed 65535");
   char* ws = static_cast<char*>(workspace);
   p.chunk_row = reinterpret_cast<int64_t*>(ws + wl.chunk_row);
+  p.fix = reinterpret_cast<longlong4*>(ws + wl.fix);
   p.rec_head = ws + wl.head;
   p.rec_tail = ws + wl.tail;
   p.arg_head = rk == RK_MINMAX ? reinterpret_cast<int64_t*>(ws + wl.arg_head) : nullptr;
@@ -98,7 +100,7 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
                  !std::getenv("OGN_ENGINE_NO_SHORT");
   {
     TimedLaunch t((n + "_chunk_rows").c_str(), s);
-    const dim3 g((unsigned)((p.m + 255) / 256), (unsigned)ptr_batches);
+    const dim3 g((unsigned)((pl.nchunks + 255) / 256), (unsigned)ptr_batches);
     if (i64) hipLaunchKernelGGL(chunk_rows_kernel<int64_t>, g, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(chunk_rows_kernel<int32_t>, g, dim3(256), 0, s, p);
   }
