@@ -834,13 +834,15 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   const int64_t b = blockIdx.z;
   const int64_t pb = p.ptr_bstride ? b : 0;
   const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr) + pb * p.ptr_bstride;
+  // The row that starts inside chunk c and ends past it, from the chunk-row
+  // pass (one load instead of chunk_row -> ptr[r] -> ptr[r + 1]).  Loaded
+  // together with ptr[0] and ptr[m] (the index is clamped into the array;
+  // entries at or past the last chunk are never used).
+  const longlong4 fx = p.fix[pb * p.nchunks + std::min<int64_t>(c, p.nchunks - 1)];
   const int64_t base = ptr[0];
   const int64_t end = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[p.m] - base, p.nnz_bound), 0);
   const int64_t nce = std::max<int64_t>(1, (end + p.chunk - 1) / p.chunk);
   if (c + 1 >= nce) return;
-  // The row that starts inside chunk c and ends past it, from the chunk-row
-  // pass (one load instead of chunk_row -> ptr[r] -> ptr[r + 1]).
-  const longlong4 fx = p.fix[pb * p.nchunks + c];
   if (fx.x < 0 || fx.x >= p.m) return;
   const int64_t r = fx.x, rs = fx.y, re = fx.z;
   const int64_t c2 = std::min<int64_t>((re - 1 - base) / p.chunk, nce - 1);
