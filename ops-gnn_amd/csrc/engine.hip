@@ -30,14 +30,15 @@ Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned, bool ga
     pl.g = 64;
     pl.tiles = (k + 63) / 64;
   }
-  // Feature traffic per wave, in whole 64-position windows: 128 KiB in
-  // contiguous mode (short rows: more, shorter chunks keep the tail small),
-  // 256 KiB in gather mode, where halving the chunk count halves the rows
-  // that cross a chunk boundary and so the fix-up pass (config 3 SpMM sum
-  // step 5.79 -> 5.70 ms, max 7.27 -> 6.96 ms; contiguous config 5 scatter
-  // got slower with 256 KiB: 1.49 -> 1.52 ms).
+  // Feature traffic per wave, in whole 64-position windows: 64 KiB in
+  // contiguous mode (short rows: more, shorter chunks keep the tail small;
+  // config 5 scatter at 256 / 384 / 512 / 1024 positions: sum 1.47 / 1.47 /
+  // 1.42 / 1.46 ms, logsumexp 2.11 / 2.01 / 1.98 / 2.05 ms), 256 KiB in
+  // gather mode, where halving the chunk count halves the rows that cross a
+  // chunk boundary and so the fix-up pass (config 3 SpMM sum step 5.79 ->
+  // 5.70 ms, max 7.27 -> 6.96 ms).
   const int64_t row_bytes = std::max<int64_t>(1, std::min<int64_t>(k, 64 * vec) * esz);
-  int64_t wave_bytes = gather ? 262144 : 131072;
+  int64_t wave_bytes = gather ? 262144 : 65536;
   if (const char* env = std::getenv("OGN_ENGINE_WAVE_KIB")) {
     const long v = std::atol(env);
     if (v >= 16) wave_bytes = (int64_t)v * 1024;
