@@ -258,7 +258,9 @@ __global__ __launch_bounds__(256) void chunk_rows_kernel(Params p) {
   const int64_t r = std::min<int64_t>(std::max<int64_t>(lo - 1, 0), p.m - 1);
   p.chunk_row[blockIdx.y * p.nchunks + c] = r;
   if (c >= 1) {
-    const int64_t rs = ptr[r], re = ptr[r + 1];
+    // ptr[r] and ptr[r + 1] from the staged window when it holds them
+    const int64_t rs = staged && r >= L && r < H ? win[r - L] : (int64_t)ptr[r];
+    const int64_t re = staged && r + 1 >= L && r + 1 < H ? win[r + 1 - L] : (int64_t)ptr[r + 1];
     const bool crosses = rs >= base + (c - 1) * p.chunk && rs < base + c * p.chunk;
     p.fix[blockIdx.y * p.nchunks + c - 1] = crosses ? make_longlong4(r, rs, re, 0) : make_longlong4(-1, 0, 0, 0);
   }
