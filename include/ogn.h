@@ -103,9 +103,11 @@ int ogn_validate_csr(const void* rowptr, const void* col, int index_dtype, int64
  *
  * mat: [batch, n, k] of in_dtype (f32/f16/bf16, or i8).  value: NULL (all
  * ones), or [nnz] (value_width 1) or [nnz, k] (value_width k), same dtype as
- * mat.  out: [batch, m, k] of out_dtype (f32/f16/bf16; i32 for i8 input,
- * accumulated exactly in int32, mean truncating toward zero, as the
- * reference's int8 path); arg: [batch, m, k] int64,
+ * mat.  out: [batch, m, k] of out_dtype, by the reference's table
+ * (torch_sparse_spmm.cpp:88-90): f32 -> f32; f16 -> f32 | f16;
+ * bf16 -> f32 | bf16; i8 -> i32 | f32.  i8 sums accumulate exactly in int32;
+ * an i32 mean truncates toward zero, an f32 mean is the exact quotient
+ * rounded once.  Other pairs return OGN_EUNSUPPORTED.  arg: [batch, m, k] int64,
  * required for min/max, ignored otherwise.  Arithmetic is fp32 (min/max of
  * fp32 inputs compare exact fp64 products).  min/max ignore NaN products,
  * the first edge wins ties, and an empty or all-NaN row gives 0 / arg = nnz.

@@ -4,7 +4,8 @@
 
 Every ``csrc/*.hip`` file is compiled separately with hipcc for gfx950 and the
 objects are linked into ``ops_gnn/libogn_hip.so`` next to the Python package
-that loads it.  Packed-fp32 instruction selection is disabled for all device
+that loads it.  ``csrc/pybind.cpp`` (host C++) becomes the torch extension
+``ops_gnn/_pybind.so`` over that library.  Packed-fp32 instruction selection is disabled for all device
 code (``-packed-fp32-ops``).
 """
 
@@ -89,9 +90,46 @@ def build(jobs: int = 8, verbose: bool = True, incremental: bool = False) -> Pat
     return target
 
 
+EXT_NAME = "_pybind"
+
+
+def build_extension(verbose: bool = True) -> Path:
+    """Compile csrc/pybind.cpp (host C++, no device code) into the torch
+    extension ops_gnn/_pybind.so, linked against libogn_hip.so (found next to
+    it through an $ORIGIN rpath) and torch's libraries."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    target = OUT_DIR / (EXT_NAME + ".so")
+    tmp = target.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-w",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-DTORCH_EXTENSION_NAME={EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           *[f"-I{p}" for p in cpp_extension.include_paths(device_type="cuda")],
+           f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include",
+           str(CSRC / "pybind.cpp"), "-o", str(tmp),
+           f"-L{OUT_DIR}", "-logn_hip", "-Wl,-rpath,$ORIGIN",
+           f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+           f"-Wl,-rpath,{torch_lib}"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"extension build failed:\n{proc.stderr}")
+    os.replace(tmp, target)
+    if verbose:
+        print(f"built {target}")
+    return target
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", "--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("--incremental", action="store_true", help="recompile only out-of-date objects")
+    ap.add_argument("--extension-only", action="store_true", help="rebuild only the torch extension")
     args = ap.parse_args()
-    build(args.jobs, incremental=args.incremental)
+    if not args.extension_only:
+        build(args.jobs, incremental=args.incremental)
+    build_extension()

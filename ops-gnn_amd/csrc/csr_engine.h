@@ -143,6 +143,19 @@ __device__ __forceinline__ void lse_add(float& m, float& s, float x) {
   m = nm;
 }
 
+// int8 SpMM sum / mean from the exact int32 sum: an int32 output truncates
+// the mean toward zero; an fp32 output takes the exact sum, or the quotient
+// rounded once (fp64 divide, then one rounding to fp32).
+__device__ __forceinline__ void finish_int(const Params& p, int64_t off, int32_t a, int64_t cnt) {
+  const bool mean = p.reduce == OGN_REDUCE_MEAN;
+  if (p.out_dt == OGN_I32) {
+    static_cast<int32_t*>(p.out)[off] = mean ? (cnt > 0 ? a / (int32_t)cnt : 0) : a;
+  } else {
+    const double v = mean ? (cnt > 0 ? (double)a / (double)cnt : 0.0) : (double)a;
+    static_cast<float*>(p.out)[off] = (float)v;
+  }
+}
+
 // Finish one output element from its combined partial state.
 //   sum kinds: a = sum (or product); mean divides by the row length.
 //   min/max: (best, barg) resolved against the seed of the mode.
@@ -231,7 +244,8 @@ __global__ __launch_bounds__(256) void chunk_rows_kernel(Params p) {
   const int64_t c = cb + threadIdx.x;
   const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr) + blockIdx.y * p.ptr_bstride;
   const int64_t base = ptr[0];
-  const int64_t total = std::max<int64_t>((int64_t)ptr[p.m] - base, 0);
+  // the data end, computed as engine_kernel and fixup_kernel compute it
+  const int64_t total = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[p.m] - base, p.nnz_bound), 0);
   const int64_t nce = std::min<int64_t>(p.nchunks, (total + p.chunk - 1) / p.chunk);
   if (cb >= nce) return;  // whole block
   const int64_t clast = std::min<int64_t>(cb + (int64_t)blockDim.x - 1, nce - 1);
@@ -574,13 +588,10 @@ void engine_kernel(Params p) {
       int64_t ag[NE];
       const int64_t off = b * p.out_bstride + r * K + k0;
       if constexpr (IS_INT && RK == RK_SUM) {
-        // integer sum / mean (mean truncates toward zero), int32 output
-        const int32_t cnt = (int32_t)(re - rs);
-        int32_t* o = static_cast<int32_t*>(p.out) + off;
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
           if (!VL && k0 + i >= K) break;
-          o[i] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? acc[i] / cnt : 0) : acc[i];
+          finish_int(p, off + i, acc[i], re - rs);
         }
       } else {
 #pragma unroll
@@ -803,7 +814,7 @@ void engine_kernel(Params p) {
 // hundreds of chunks is folded by every lane of the wave, not only by the K
 // lanes of its features.  Merges of min/max partials compare (value,
 // position), so the tie rules hold whatever the fold order.
-// INT: int32 sum records and an int32 output (int8 SpMM).
+// INT: int32 sum records (int8 SpMM), finished by finish_int.
 template <typename MT>
 __device__ __forceinline__ void mm_merge(MT& best, int64_t& barg, MT ob, int64_t oa, bool is_min, bool later,
                                          bool nanprop) {
@@ -944,8 +955,7 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
         const int64_t k = k0 + f * kWave;
         const int64_t off = b * p.out_bstride + r * K + k;
         if constexpr (INT && RK == RK_SUM) {
-          const int32_t cnt = (int32_t)(re - rs);
-          static_cast<int32_t*>(p.out)[off] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? a[f] / cnt : 0) : a[f];
+          finish_int(p, off, a[f], re - rs);
           continue;
         }
         float v;
@@ -1048,8 +1058,7 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
     if (g != 0) continue;
     const int64_t off = b * p.out_bstride + r * K + k;
     if constexpr (INT && RK == RK_SUM) {
-      const int32_t cnt = (int32_t)(re - rs);
-      static_cast<int32_t*>(p.out)[off] = p.reduce == OGN_REDUCE_MEAN ? (cnt > 0 ? a / cnt : 0) : a;
+      finish_int(p, off, a, re - rs);
       continue;
     }
     float v;

@@ -60,18 +60,14 @@ static int spmm_impl(const void* rowptr, const void* col, int index_dtype, const
     return fail(OGN_EINVAL, "ogn_spmm_csr: negative size");
   if (index_dtype != OGN_I32 && index_dtype != OGN_I64)
     return fail(OGN_EINVAL, "ogn_spmm_csr: index dtype must be int32 or int64");
-  if (in_dtype == OGN_I8) {
-    // torch_sparse int8 SpMM: int32 accumulation and output
-    if (out_dtype != OGN_I32)
-      return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr: int8 mat needs an int32 output");
-    if (message_op != OGN_MSG_MUL || semantics != OGN_SPMM_TORCH_SPARSE)
-      return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr: int8 supports torch_sparse x * w messages only");
-  } else {
-    if (in_dtype != OGN_F32 && in_dtype != OGN_F16 && in_dtype != OGN_BF16)
-      return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr: mat dtype must be float32, float16, bfloat16 or int8");
-    if (out_dtype != OGN_F32 && out_dtype != OGN_F16 && out_dtype != OGN_BF16)
-      return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr: out dtype must be float32, float16 or bfloat16");
-  }
+  // Input -> output dtype table of the reference (torch_sparse_spmm.cpp:88-90):
+  // f32 -> f32; f16 -> f32|f16; bf16 -> f32|bf16; int8 -> f32|int32.
+  if (in_dtype != OGN_F32 && in_dtype != OGN_F16 && in_dtype != OGN_BF16 && in_dtype != OGN_I8)
+    return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr: mat dtype must be float32, float16, bfloat16 or int8");
+  if (!(out_dtype == OGN_F32 || (in_dtype == OGN_I8 ? out_dtype == OGN_I32 : out_dtype == in_dtype)))
+    return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr: unsupported input/output dtype combination");
+  if (in_dtype == OGN_I8 && (message_op != OGN_MSG_MUL || semantics != OGN_SPMM_TORCH_SPARSE))
+    return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr: int8 supports torch_sparse x * w messages only");
   if (reduce < OGN_REDUCE_SUM || reduce > OGN_REDUCE_MAX)
     return fail(OGN_EINVAL, "ogn_spmm_csr: reduce must be sum/mean/min/max");
   const bool mm = reduce >= OGN_REDUCE_MIN;

@@ -18,8 +18,16 @@ from ._lib import check, dptr, lib, stream_of
 
 SPMM_INPUT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.int8)
 SPMM_OUTPUT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.int32)
-# int8 mat / value give an int32 result (reference python/ops_gnn/torch_sparse_spmm.py:213)
 SPMM_FLOAT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+# Output dtypes each mat dtype may produce (reference
+# csrc/npu/torch_sparse_spmm/op_host/torch_sparse_spmm.cpp:88-90); the first
+# one is the default (python/ops_gnn/torch_sparse_spmm.py:213).
+SPMM_OUTPUTS_FOR = {
+    torch.float32: (torch.float32,),
+    torch.float16: (torch.float16, torch.float32),
+    torch.bfloat16: (torch.bfloat16, torch.float32),
+    torch.int8: (torch.int32, torch.float32),
+}
 
 
 def _index_code(t: torch.Tensor) -> int:
@@ -61,8 +69,8 @@ def spmm_forward(ptr: torch.Tensor, col: torch.Tensor, value: Optional[torch.Ten
     """
     if mat.dtype not in SPMM_INPUT_DTYPES:
         raise ValueError("mat must be float32, float16, bfloat16 or int8")
-    if out_dtype not in SPMM_OUTPUT_DTYPES or ((mat.dtype == torch.int8) != (out_dtype == torch.int32)):
-        raise ValueError("unsupported output dtype (int8 input gives int32, float inputs a float dtype)")
+    if out_dtype not in SPMM_OUTPUTS_FOR[mat.dtype]:
+        raise ValueError("unsupported input/output dtype combination")
     mat = mat.contiguous()
     ptr = ptr.contiguous()
     col = col.contiguous()
@@ -181,19 +189,26 @@ class _VersionCache:
 INDEX_FACTS = _VersionCache()
 
 
+def index_probe(index: torch.Tensor) -> Tuple[bool, int, int]:
+    """(unsorted, min, max) of a nonempty int32 / int64 index in one device
+    pass and one 24-byte device-to-host read; not cached."""
+    idx = index.contiguous()
+    if idx.dtype != torch.int64:
+        idx = idx.to(torch.int64)
+    facts = torch.empty(3, dtype=torch.int64, device=idx.device)
+    check(lib.ogn_index_facts(dptr(idx), idx.numel(), dptr(facts), stream_of(idx)), "index facts")
+    unsorted, mn, mx = facts.tolist()
+    return (unsorted != 0, mn, mx)
+
+
 def index_facts(index: torch.Tensor, key: Optional[torch.Tensor] = None) -> Tuple[bool, int, int]:
-    """(sorted, min, max) of an int32 / int64 index; one 24-byte
-    device-to-host read, cached per tensor version of `key` (default: `index`
-    itself; pass the caller's tensor when `index` is a fresh view of it)."""
+    """(sorted, min, max) of an int32 / int64 index (index_probe), cached per
+    tensor version of `key` (default: `index` itself; pass the caller's
+    tensor when `index` is a fresh view of it)."""
 
     def compute():
-        idx = index.contiguous()
-        if idx.dtype != torch.int64:
-            idx = idx.to(torch.int64)
-        facts = torch.empty(3, dtype=torch.int64, device=idx.device)
-        check(lib.ogn_index_facts(dptr(idx), idx.numel(), dptr(facts), stream_of(idx)), "index facts")
-        unsorted, mn, mx = facts.tolist()
-        return (unsorted == 0, mn, mx)
+        unsorted, mn, mx = index_probe(index)
+        return (not unsorted, mn, mx)
 
     return INDEX_FACTS.get(index if key is None else key, compute)
 

@@ -93,12 +93,21 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
             if d != dim:
                 line = line.select(d, 0)
         compact = line.numel() == src.size(dim)
+    # Exact index bounds (one cached device probe per index version); both
+    # paths below rely on every index lying in [0, size) (reference
+    # python/ops_gnn/scatter.py:406-422, same errors).
+    checked = index.numel() > 0 and expanded.numel() > 0
+    mn, mx = _native.index_facts(line, key=index)[1:] if checked else (0, -1)
+    if mn < 0:
+        raise IndexError(f"index contains a negative value ({mn})")
     if out is not None:
         size = out.size(dim)
     elif dim_size is not None:
         size = int(dim_size)
     else:
-        size = (_native.index_facts(line, key=index)[2] + 1) if index.numel() else 0
+        size = mx + 1
+    if mx >= size:
+        raise IndexError(f"index value {mx} is out of bounds for output size {size} at dimension {dim}")
     shape = list(src.shape)
     shape[dim] = size
     if out is not None:
@@ -118,9 +127,8 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
     src3 = src.contiguous().reshape(before, length, after)
     arg3 = None
     use_segments = False
-    if compact and index.numel() > 0:
-        is_sorted, mn, mx = _native.index_facts(line, key=index)
-        use_segments = is_sorted and mn >= 0 and mx < size
+    if compact and checked:
+        use_segments = _native.index_facts(line, key=index)[0]
     if use_segments:
         ptr = _native.sorted_index_ptr(index, size, line.reshape(1, -1))
         res3, arg3 = _native.segment_reduce(src3, ptr, size, code, _lib.SEM_SCATTER, out3, has_out, is_minmax)

@@ -320,6 +320,28 @@ def sddmm(ptr, col, lhs, rhs, op="dot", lhs_target=0, rhs_target=2):
 DGL_MSG = {"copy_lhs": 0, "add": 1, "sub": 2, "mul": 3, "div": 4, "copy_rhs": 5}
 
 
+# Input -> output dtype pairs of torch_sparse SpMM (reference golden
+# test/torch_sparse_spmm/arch35/golden.py:80-88, COMBOS).
+SPMM_DTYPE_COMBOS = (("float32", "float32"), ("float16", "float16"), ("bfloat16", "bfloat16"),
+                     ("float16", "float32"), ("bfloat16", "float32"), ("int8", "int32"), ("int8", "float32"))
+
+
+def spmm_output_cast(out, out_dtype):
+    """The golden's final cast of the fp64 result (reference
+    test/torch_sparse_spmm/arch35/golden.py:114-115): an int32 output
+    truncates toward zero; every other output is one rounding of the fp64
+    value.  `out_dtype` is a numpy dtype name; 'bfloat16' returns the fp64
+    values rounded to bf16 (as float32 numbers)."""
+    name = str(out_dtype).replace("torch.", "")
+    out = np.asarray(out, dtype=np.float64)
+    if name == "int32":
+        return np.trunc(out).astype(np.int32)
+    if name == "bfloat16":
+        import torch
+        return torch.from_numpy(out).to(torch.bfloat16).float().numpy()
+    return out.astype(np.dtype(name))
+
+
 def spmm_dgl(ptr, col, x, rhs, op, reduce):
     """DGL-style aggregation (reference test/unified_spmm/arch22/golden.py:13-92).
 

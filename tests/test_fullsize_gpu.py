@@ -10,11 +10,16 @@ depend on size:
   the row exceeds it. arg is the first edge attaining it; this is checked
   against a torch scatter_reduce(amin) over all 7.9 G edge-feature products.
 - segment_csr (config 2): the full output is compared with the oracle.
-- scatter (config 5): sampled nodes are compared with the oracle, and the
-  per-feature totals must match.
+- SpMM min is checked like max; bf16 sum by linearity at 1e-2 and sampled
+  rows against the oracle on the same bf16 inputs.
+- scatter (config 5): sum / mean / max at sampled nodes (hubs included)
+  against the oracle, plus per-feature totals; scatter_log_softmax and
+  scatter_logsumexp at sampled nodes against the oracle, and exp(log_softmax)
+  summing to 1 in every group.
 - GAT layer (config 4): sampled edges of the sddmm are compared with fp64
-  dots, every softmax group must sum to 1, and sampled rows of the SpMM are
-  compared with the oracle.
+  dots; every softmax group must sum to 1, and the softmax of sampled rows
+  (hubs included) is compared edge by edge with the oracle; sampled rows of
+  the SpMM are compared with the oracle.
 
 Tolerances as elsewhere: sums |a - g| <= rtol * sum|terms| (rtol 1e-5 fp32,
 1e-2 fp16); extrema and args bit-exact.
@@ -85,9 +90,10 @@ def test_config3_spmm_sum_full_size(ogn, oracle, cfg3):
     assert float(err.max()) <= 0, f"config-3 C w differs from A (B w): worst excess {float(err.max()):.3e}"
 
 
-def test_config3_spmm_max_full_size(ogn, oracle, cfg3):
+@pytest.mark.parametrize("reduce", ["max", "min"])
+def test_config3_spmm_extremum_full_size(ogn, oracle, cfg3, reduce):
     (ptr, col, val, mat), d = cfg3
-    vals, arg = ogn.csr_spmm(d["ptr"], d["col"], d["val"], d["mat"], "max")
+    vals, arg = ogn.csr_spmm(d["ptr"], d["col"], d["val"], d["mat"], reduce)
     m, k = vals.shape
     e = col.size
     deg = d["ptr"][1:] - d["ptr"][:-1]
@@ -96,15 +102,15 @@ def test_config3_spmm_max_full_size(ogn, oracle, cfg3):
     lo = d["ptr"][:-1].unsqueeze(1)
     hi = d["ptr"][1:].unsqueeze(1)
     ok = ((arg >= lo) & (arg < hi)) | (empty.unsqueeze(1) & (arg == e))
-    assert bool(ok.all()), "config-3 max arg outside its row"
+    assert bool(ok.all()), f"config-3 {reduce} arg outside its row"
     # value attained by arg, exactly: the kernel compares exact fp64 products
     # and rounds the winner once
     a = arg.clamp(max=e - 1)
     best64 = d["val"].double()[a] * d["mat"].double()[d["col"][a], torch.arange(k, device=DEV)]
     attained = best64.float()
     attained[empty] = 0
-    assert torch.equal(attained, vals), "config-3 max value not val[arg] * B[col[arg]]"
-    # maximal over all edges, first edge among ties: amin of attaining edge ids
+    assert torch.equal(attained, vals), f"config-3 {reduce} value not val[arg] * B[col[arg]]"
+    # extremal over all edges, first edge among ties: amin of attaining edge ids
     row_of = torch.repeat_interleave(torch.arange(m, device=DEV), deg)
     first = torch.full((m, k), e, dtype=torch.int64, device=DEV)
     step = 1 << 22
@@ -112,21 +118,52 @@ def test_config3_spmm_max_full_size(ogn, oracle, cfg3):
         sl = slice(s, min(s + step, e))
         prod = d["val"][sl].double().unsqueeze(1) * d["mat"][d["col"][sl]].double()
         best = best64[row_of[sl]]
-        assert bool((prod <= best).all()), "config-3 an edge exceeds the max"
+        beyond = prod > best if reduce == "max" else prod < best
+        assert not bool(beyond.any()), f"config-3 an edge beats the {reduce}"
         ids = torch.arange(s, sl.stop, device=DEV).unsqueeze(1).expand(-1, k)
         cand = torch.where(prod == best, ids, torch.full_like(ids, e))
         first.scatter_reduce_(0, row_of[sl].unsqueeze(1).expand(-1, k), cand, "amin")
-        del prod, best, ids, cand
-    assert torch.equal(first, arg), "config-3 max arg is not the first maximising edge"
+        del prod, best, ids, cand, beyond
+    assert torch.equal(first, arg), f"config-3 {reduce} arg is not the first extremal edge"
     # sampled rows against the oracle, bit-exact
     rows = _sample_rows(ptr, np.random.default_rng(32), hubs=16, rand=200)
     sp, sc, sv = _sub_csr(ptr, col, val, rows)
-    gold, garg = oracle.spmm_csr(sp, sc, sv, mat, "max")
-    assert_exact(vals[torch.from_numpy(rows).to(DEV)], gold.astype(np.float32), "config-3 sampled max values")
+    gold, garg = oracle.spmm_csr(sp, sc, sv, mat, reduce)
+    assert_exact(vals[torch.from_numpy(rows).to(DEV)], gold.astype(np.float32), f"config-3 sampled {reduce} values")
     base = ptr[rows][:, None]
     sub_base = sp[:-1][:, None]
     expect_arg = np.where(garg == sc.size, e, garg - sub_base + base)
-    assert_exact(arg[torch.from_numpy(rows).to(DEV)], expect_arg, "config-3 sampled max args")
+    assert_exact(arg[torch.from_numpy(rows).to(DEV)], expect_arg, f"config-3 sampled {reduce} args")
+
+
+def test_config3_spmm_sum_bf16_full_size(ogn, oracle, cfg3):
+    """Config 3 in bf16 (values cast to bf16 like the mat): linearity over
+    every row at the bf16 tolerance 1e-2, and sampled hub / random rows
+    against the oracle on the same bf16 inputs."""
+    (ptr, col, val, mat), d = cfg3
+    vb, mb = d["val"].bfloat16(), d["mat"].bfloat16()
+    out = ogn.csr_spmm(d["ptr"], d["col"], vb, mb, "sum")
+    assert out.dtype == torch.bfloat16
+    rows = _sample_rows(ptr, np.random.default_rng(35))
+    sp, sc, _ = _sub_csr(ptr, col, val, rows)
+    sel = torch.from_numpy(np.concatenate([np.arange(ptr[r], ptr[r + 1]) for r in rows])).to(DEV)
+    sv = vb[sel].float().cpu().numpy()
+    mf = mb.float().cpu().numpy()
+    gold, _ = oracle.spmm_csr(sp, sc, sv, mf, "sum")
+    scale, _ = oracle.spmm_csr(sp, sc, np.abs(sv), np.abs(mf), "sum")
+    assert_sum_close(out[torch.from_numpy(rows).to(DEV)], gold, scale, torch.bfloat16, "config-3 bf16 sampled rows")
+    w = torch.randn(mat.shape[1], dtype=torch.float64, device=DEV, generator=torch.Generator(DEV).manual_seed(6))
+    m = ptr.size - 1
+    row_of = torch.repeat_interleave(torch.arange(m, device=DEV), d["ptr"][1:] - d["ptr"][:-1])
+    bw = mb.double() @ w
+    babs = mb.double().abs() @ w.abs()
+    ref = torch.zeros(m, dtype=torch.float64, device=DEV).index_add_(0, row_of, vb.double() * bw[d["col"]])
+    bound = torch.zeros(m, dtype=torch.float64, device=DEV).index_add_(0, row_of, vb.double().abs() * babs[d["col"]])
+    # the output rounds each element to bf16 once: |C - C_exact| <= 2^-8 |C|
+    got = out.double() @ w
+    round_bound = (out.double().abs() @ w.abs()) * 2.0 ** -8
+    err = (got - ref).abs() - (1e-2 * bound + round_bound + 1e-3)
+    assert float(err.max()) <= 0, f"config-3 bf16 C w differs from A (B w): worst excess {float(err.max()):.3e}"
 
 
 def test_config2_segment_full_size(ogn, oracle):
@@ -148,31 +185,39 @@ def test_config2_segment_full_size(ogn, oracle):
     np.testing.assert_allclose(lse.cpu().numpy(), gold, rtol=1e-5, atol=1e-5)
 
 
-def test_config5_scatter_full_size(ogn, oracle):
+@pytest.fixture(scope="module")
+def cfg5():
     from ops_gnn.synthetic import cfg5_coo_scatter
 
     idx, src = cfg5_coo_scatter()
+    return idx, src, torch.from_numpy(idx).to(DEV), torch.from_numpy(src).to(DEV)
+
+
+def _cfg5_nodes(ptr_np, nodes, seed):
+    rng = np.random.default_rng(seed)
+    deg = np.diff(ptr_np)
+    return np.unique(np.concatenate([np.argsort(deg)[-8:], rng.integers(0, nodes, 300), [0, nodes - 1]]))
+
+
+def test_config5_scatter_full_size(ogn, oracle, cfg5):
+    idx, src, index, s = cfg5
     nodes = 1_000_000
-    index = torch.from_numpy(idx).to(DEV)
-    s = torch.from_numpy(src).to(DEV)
     ptr = ogn.ind2ptr(index, nodes)
     assert torch.equal(ogn.ptr2ind(ptr, idx.size), index), "config-5 ind2ptr / ptr2ind round trip"
     ptr_np = ptr.cpu().numpy()
-    rng = np.random.default_rng(33)
-    deg = np.diff(ptr_np)
-    nodes_pick = np.unique(np.concatenate([np.argsort(deg)[-8:], rng.integers(0, nodes, 300)]))
-    for reduce in ("sum", "max"):
+    nodes_pick = _cfg5_nodes(ptr_np, nodes, 33)
+    for reduce in ("sum", "mean", "max"):
         res = ogn.scatter(s, index, 0, dim_size=nodes, reduce=reduce)
-        got, arg = (res, None) if reduce == "sum" else ogn.scatter_max(s, index, 0, None, nodes)
+        got, arg = (res, None) if reduce != "max" else ogn.scatter_max(s, index, 0, None, nodes)
         for n in nodes_pick:
             a, b = ptr_np[n], ptr_np[n + 1]
             sub = src[a:b]
-            if reduce == "sum":
-                gold = sub.astype(np.float64).sum(0)
-                err = np.abs(got[n].double().cpu().numpy() - gold) - (1e-5 * np.abs(sub).sum(0) + 1e-6)
-                assert (err <= 0).all(), f"config-5 sum node {n}"
+            if reduce != "max":
+                gv, _ = oracle.scatter(sub, np.zeros((b - a, 1), np.int64), 0, 1, reduce)
+                sv, _ = oracle.scatter(np.abs(sub), np.zeros((b - a, 1), np.int64), 0, 1, reduce)
+                assert_sum_close(got[n:n + 1], gv, sv, torch.float32, f"config-5 {reduce} node {n}")
             else:
-                gv, ga = oracle.scatter(sub, np.zeros((b - a, 1), np.int64) + 0, 0, 1, "max")
+                gv, ga = oracle.scatter(sub, np.zeros((b - a, 1), np.int64), 0, 1, "max")
                 assert_exact(got[n:n + 1], gv.astype(np.float32), f"config-5 max node {n}")
                 want = np.where(ga == (b - a), idx.size, ga + a)
                 assert_exact(arg[n:n + 1], want, f"config-5 max arg node {n}")
@@ -181,6 +226,38 @@ def test_config5_scatter_full_size(ogn, oracle):
             ref = s.double().sum(0)
             bound = 1e-5 * s.double().abs().sum(0) + 1e-6
             assert bool(((tot - ref).abs() <= bound).all()), "config-5 per-feature totals"
+        if reduce == "mean":
+            deg = torch.from_numpy(np.diff(ptr_np)).to(DEV).double().unsqueeze(1)
+            tot = (got.double() * deg).sum(0)
+            ref = s.double().sum(0)
+            bound = 1e-5 * s.double().abs().sum(0) + 1e-4
+            assert bool(((tot - ref).abs() <= bound).all()), "config-5 mean x degree totals"
+        del res, got, arg
+
+
+@pytest.mark.parametrize("mode", ["log_softmax", "logsumexp"])
+def test_config5_grouped_full_size(ogn, oracle, cfg5, mode):
+    """scatter_log_softmax / scatter_logsumexp at 50 M x 32: sampled nodes
+    (the 8 largest hubs included) against the oracle at 1e-5, and, over all
+    rows, exp(log_softmax) summing to 1 per (node, feature)."""
+    idx, src, index, s = cfg5
+    nodes = 1_000_000
+    ptr_np = ogn.ind2ptr(index, nodes).cpu().numpy()
+    fn = ogn.scatter_log_softmax if mode == "log_softmax" else ogn.scatter_logsumexp
+    got = fn(s, index, 0, nodes)
+    for n in _cfg5_nodes(ptr_np, nodes, 36):
+        a, b = ptr_np[n], ptr_np[n + 1]
+        gold = oracle.group_softmax(src[a:b], np.zeros(b - a, np.int64), 0, 1, mode)
+        part = got[a:b] if mode == "log_softmax" else got[n:n + 1]
+        g = part.cpu().numpy()
+        if b == a and mode == "logsumexp":
+            assert np.isneginf(g).all(), f"config-5 logsumexp empty node {n}"
+            continue
+        np.testing.assert_allclose(g, gold, rtol=1e-5, atol=1e-5, err_msg=f"config-5 {mode} node {n}")
+    if mode == "log_softmax":
+        sums = torch.zeros((nodes, s.shape[1]), dtype=torch.float64, device=DEV).index_add_(0, index, got.double().exp())
+        nonempty = torch.from_numpy(np.diff(ptr_np) > 0).to(DEV)
+        assert bool(((sums[nonempty] - 1).abs() <= 1e-4).all()), "config-5 exp(log_softmax) group sums"
 
 
 def test_config4_gat_layer_full_size(ogn, oracle):
@@ -205,8 +282,19 @@ def test_config4_gat_layer_full_size(ogn, oracle):
     sums = torch.zeros(n, dtype=torch.float64, device=DEV).index_add_(0, row, att.double())
     nonempty = (dp[1:] - dp[:-1]) > 0
     assert torch.allclose(sums[nonempty], torch.ones_like(sums[nonempty]), atol=2e-2), "config-4 softmax sums"
-    out = ogn.csr_spmm(dp, dc, att, dv, "sum")
+    # sampled rows (hubs included), every edge against the oracle's grouped
+    # softmax of the same fp16 scores, fp16 tolerance 1e-2
     rows = _sample_rows(ptr, rng, hubs=8, rand=200)
+    sc_all = scores.float().cpu().numpy()
+    att_all = att.float().cpu().numpy()
+    for r in rows:
+        a, b = ptr[r], ptr[r + 1]
+        if a == b:
+            continue
+        gold = oracle.group_softmax(sc_all[a:b], np.zeros(b - a, np.int64), 0, 1, "softmax")
+        gold = torch.from_numpy(gold).half().float().numpy()
+        np.testing.assert_allclose(att_all[a:b], gold, rtol=1e-2, atol=1e-2, err_msg=f"config-4 softmax row {r}")
+    out = ogn.csr_spmm(dp, dc, att, dv, "sum")
     sp, sc, sa = _sub_csr(ptr, col, att.float().cpu().numpy(), rows)
     gold, _ = oracle.spmm_csr(sp, sc, sa, dv.float().cpu().numpy(), "sum")
     scale, _ = oracle.spmm_csr(sp, sc, np.abs(sa), np.abs(dv.float().cpu().numpy()), "sum")

@@ -134,6 +134,37 @@ def test_spmm_matches_brute_force_with_ties_and_nans(reduce):
         np.testing.assert_array_equal(arg, ref_arg)
 
 
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("out_dtype", ["int32", "float32"])
+def test_spmm_int8_output_cast_brute_force(reduce, out_dtype):
+    """int8 SpMM to int32 or float32 (reference golden.py:80-88,114-115):
+    exact integer arithmetic with Python ints / Fractions, an int32 mean
+    truncated toward zero, a float32 mean rounded from the exact quotient."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(7)
+    ptr, col = _random_csr(rng, 40, 11, 6)
+    mat = rng.integers(-128, 128, size=(11, 3)).astype(np.int8)
+    val = rng.integers(-128, 128, size=col.size).astype(np.int8)
+    out, arg = orc.spmm_csr(ptr, col, val, mat, reduce)
+    got = orc.spmm_output_cast(out, out_dtype)
+    assert got.dtype == np.dtype(out_dtype)
+    for r in range(len(ptr) - 1):
+        for j in range(3):
+            terms = [int(mat[col[e], j]) * int(val[e]) for e in range(ptr[r], ptr[r + 1])]
+            if not terms:
+                exact = Fraction(0)
+            elif reduce == "sum":
+                exact = Fraction(sum(terms))
+            elif reduce == "mean":
+                exact = Fraction(sum(terms), len(terms))
+            else:
+                exact = Fraction(min(terms) if reduce == "min" else max(terms))
+            want = int(exact) if out_dtype == "int32" else np.float32(float(exact))
+            assert got[r, j] == want, (r, j, reduce, out_dtype)
+    assert ("int8", "float32") in orc.SPMM_DTYPE_COMBOS and ("float32", "float16") not in orc.SPMM_DTYPE_COMBOS
+
+
 # ----------------------------------------------------------------- ind2ptr / ptr2ind
 # Input tables: reference test/sparse/arch35/test_sparse.py:261-282 and :299-315.
 IND2PTR_CASES = [

@@ -299,3 +299,31 @@ def test_grouped_softmax_errors(ogn):
         ogn.scatter_softmax(src.double(), torch.zeros(6, dtype=torch.long, device="cuda"))
     with pytest.raises(IndexError):
         ogn.scatter_softmax(src, torch.zeros(6, dtype=torch.long, device="cuda"), dim=3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.int32, torch.int64, torch.uint8])
+@pytest.mark.parametrize("layout", ["sorted", "unsorted", "full_shape"])
+@pytest.mark.parametrize("reduce", ["sum", "max"])
+def test_index_out_of_range_raises(ogn, dtype, layout, reduce):
+    """A negative index, or one at or past the output size, raises IndexError
+    on every path (reference python/ops_gnn/scatter.py:406-422); nothing is
+    silently dropped."""
+    src = torch.arange(12, device="cuda").reshape(6, 2).to(dtype)
+    base = [0, 0, 1, 2, 2, 3] if layout == "sorted" else [2, 0, 3, 1, 0, 2]
+
+    def make(values):
+        idx = torch.tensor(values, device="cuda")
+        return idx.view(-1, 1).expand(6, 2).contiguous() if layout == "full_shape" else idx
+
+    bad_neg = list(base)
+    bad_neg[3] = -1
+    with pytest.raises(IndexError, match="negative value \\(-1\\)"):
+        ogn.scatter(src, make(bad_neg), dim=0, reduce=reduce)
+    with pytest.raises(IndexError, match="index value 3 is out of bounds for output size 3 at dimension 0"):
+        ogn.scatter(src, make(base), dim=0, dim_size=3, reduce=reduce)
+    out = torch.zeros(2, 2, device="cuda").to(dtype)
+    with pytest.raises(IndexError, match="out of bounds for output size 2"):
+        ogn.scatter(src, make(base), dim=0, out=out, reduce=reduce)
+    # in range: dim_size = max + 1 is accepted
+    ok = ogn.scatter(src, make(base), dim=0, dim_size=4, reduce=reduce)
+    assert ok.shape == (4, 2)

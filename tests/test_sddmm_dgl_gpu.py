@@ -109,9 +109,13 @@ def test_dgl_copy_lhs(ogn, oracle, dtype, reduce, index_dtype):
         assert_sum_close(got, gold, scale, dtype, f"dgl/{reduce}")
 
 
-@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "copy_rhs"])
+# copy_rhs aggregates the edge features as given: only the full edge shape
+_MSG_CASES = [(op, shape) for op in ("add", "sub", "mul", "div") for shape in ("scalar", "column", "full")] + \
+    [("copy_rhs", "full")]
+
+
+@pytest.mark.parametrize("op,edge_shape", _MSG_CASES)
 @pytest.mark.parametrize("reduce", ["sum", "mean", "max", "min"])
-@pytest.mark.parametrize("edge_shape", ["scalar", "column", "full"])
 def test_dgl_binary_messages(ogn, oracle, op, reduce, edge_shape):
     ptr, col, rng = _csr(200, 150, 6, seed=6)
     nnz = col.numel()
@@ -119,8 +123,6 @@ def test_dgl_binary_messages(ogn, oracle, op, reduce, edge_shape):
     w_full = torch.from_numpy((rng.standard_normal((nnz, 8)) + 3).astype(np.float32))
     w = {"scalar": w_full[:, 0].contiguous(), "column": w_full[:, :1].contiguous(), "full": w_full}[edge_shape]
     if op == "copy_rhs":
-        if edge_shape != "full":
-            pytest.skip("copy_rhs aggregates the edge features as given")
         got = ogn.spmm(ptr.cuda(), col.cuda(), None, op="copy_rhs", reduce=reduce, rhs=w.cuda())
         gold = oracle.spmm_dgl(ptr, col, None, w, "copy_rhs", reduce)
     else:

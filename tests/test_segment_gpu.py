@@ -139,6 +139,33 @@ def test_segment_csr_empty_and_errors(ogn):
         ogn.segment_csr(torch.ones(4, 2, dtype=torch.float64, device="cuda"), torch.tensor([0, 4], device="cuda"))
 
 
+@pytest.mark.parametrize("reduce", ["sum", "mean", "max"])
+def test_segment_csr_ends_past_source_with_chunk_crossing(ogn, oracle, reduce):
+    """Segment ends past src.size(0) are clamped (the golden slices
+    src[start:end]); the last segments, clamped, also span many wavefront
+    chunks, so the chunk-row pass, the main kernel and the fix-up must agree
+    on where the data ends."""
+    rng = np.random.default_rng(77)
+    length = 40_000
+    src = torch.from_numpy(rng.standard_normal((length, 8)).astype(np.float32))
+    lengths = rng.poisson(30, size=600)
+    ptr = np.concatenate([[0], np.cumsum(lengths)])
+    ptr = np.concatenate([ptr[ptr < length - 15_000], [length - 15_000, length - 5, length + 9_000, length + 20_000]])
+    indptr = torch.from_numpy(ptr.astype(np.int64))
+    clamped = indptr.clamp(max=length)
+    _csr_check(ogn, oracle, src, clamped, reduce, f"clamped reference/{reduce}")
+    fn = getattr(ogn, f"segment_{reduce}_csr")
+    res = fn(src.cuda(), indptr.cuda())
+    out, arg = res if isinstance(res, tuple) else (res, None)
+    gold, garg = oracle.segment_csr(src, clamped, reduce)
+    if reduce == "max":
+        assert_exact(out, cast_like(gold, src.dtype), "ends past src values")
+        assert_exact(arg, garg, "ends past src arg")
+    else:
+        scale, _ = oracle.segment_csr(src.abs(), clamped, reduce)
+        assert_sum_close(out, gold, scale, torch.float32, f"ends past src/{reduce}")
+
+
 def test_segment_reduce_and_legacy_max(ogn, oracle):
     rng = np.random.default_rng(8)
     lengths = _lengths(rng, 50, 6)

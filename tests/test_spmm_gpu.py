@@ -145,33 +145,75 @@ def test_narrow_rows_16bit(ogn, oracle, dtype, k, reduce, feature_values):
     check_spmm(ogn, oracle, ptr, col, val, mat, reduce, what=f"narrow/{dtype}/k{k}/{reduce}")
 
 
+def _check_int8(ogn, oracle, ptr, col, val, mat, reduce, out_dtype, what):
+    """int8 SpMM against the golden's cast of the fp64 result: int32 truncates,
+    float32 rounds once (reference golden.py:80-88,114-115).  Bit-exact."""
+    res = ogn.csr_spmm(ptr.cuda(), col.cuda(), None if val is None else val.cuda(), mat.cuda(), reduce,
+                       output_dtype=out_dtype)
+    got, arg = res if reduce in ("min", "max") else (res, None)
+    assert got.dtype == out_dtype
+    gold, garg = oracle.spmm_csr(ptr, col, val, mat, reduce)
+    want = oracle.spmm_output_cast(gold, out_dtype)
+    assert_exact(got, want, what + " values")
+    if arg is not None:
+        assert_exact(arg, garg, what + " arg")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.int32, torch.float32])
 @pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
 @pytest.mark.parametrize("k,feature_values", [(16, False), (128, False), (32, True), (5, False)])
-def test_int8_to_int32(ogn, oracle, reduce, k, feature_values):
+def test_int8_powerlaw(ogn, oracle, reduce, k, feature_values, out_dtype):
     # reference golden test/torch_sparse_spmm/arch35/golden.py:91-116: int8
-    # mat / value, fp64 arithmetic, trunc, int32 output; first-tie args
+    # mat / value, fp64 arithmetic, then trunc (int32) or one rounding (fp32)
     ptr, col, rng = _powerlaw(3000, 2000, 70_000, 9000, seed=20 + k)
     mat = torch.from_numpy(rng.integers(-128, 128, (2000, k)).astype(np.int8))
     shape = (col.numel(), k) if feature_values else (col.numel(),)
     val = torch.from_numpy(rng.integers(-128, 128, shape).astype(np.int8))
-    res = ogn.csr_spmm(ptr.cuda(), col.cuda(), val.cuda(), mat.cuda(), reduce)
-    got, arg = res if reduce in ("min", "max") else (res, None)
-    assert got.dtype == torch.int32
-    gold, garg = oracle.spmm_csr(ptr, col, val.float(), mat.float(), reduce)
-    want = np.trunc(gold).astype(np.int32)
-    assert_exact(got, want, f"int8/{reduce}/k{k} values")
-    if arg is not None:
-        assert_exact(arg, garg, f"int8/{reduce}/k{k} arg")
+    _check_int8(ogn, oracle, ptr, col, val, mat, reduce, out_dtype, f"int8/{reduce}/k{k}/{out_dtype}")
 
 
-def test_int8_output_dtype_contract(ogn):
+@pytest.mark.parametrize("out_dtype", [torch.int32, torch.float32])
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("batch,feature_values", [(False, False), (True, True)])
+def test_int8_sample(ogn, oracle, reduce, batch, feature_values, out_dtype):
+    # the reference's sample (golden.py:119-131) for its (int8, int32) and
+    # (int8, float32) COMBOS
+    ptr, col, _, _ = _sample(torch.float32, batch, feature_values)
+    g = torch.Generator().manual_seed(5)
+    mat = torch.randint(-128, 128, (2, 3, 4, 17) if batch else (4, 17), generator=g).to(torch.int8)
+    val = torch.randint(-128, 128, (7, 17) if feature_values else (7,), generator=g).to(torch.int8)
+    _check_int8(ogn, oracle, ptr, col, val, mat, reduce, out_dtype, f"int8 sample/{reduce}")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.int32, torch.float32])
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("features", [64, 128, 256, 512])
+def test_int8_prefetch_boundaries(ogn, oracle, reduce, features, out_dtype):
+    # reference test/torch_sparse_spmm/arch35/test_torch_sparse_spmm.py:704-716
+    # with the int8 COMBOS; the 7 / 8 / 9 / 17-edge rows give non-integer means
+    ptr = torch.tensor([0, 0, 7, 15, 24, 41], dtype=torch.int64)
+    col = torch.arange(41, dtype=torch.int64).remainder(5)
+    values = torch.arange(41).remainder(7).sub(3).to(torch.int8)
+    mat = torch.arange(5 * features).reshape(5, features).remainder(11).sub(5).to(torch.int8)
+    _check_int8(ogn, oracle, ptr, col, values, mat, reduce, out_dtype, f"int8 prefetch/{reduce}/{features}")
+
+
+def test_output_dtype_table(ogn):
+    """The reference's input -> output table (torch_sparse_spmm.cpp:88-90):
+    f32 -> f32; f16 -> f16 | f32; bf16 -> bf16 | f32; int8 -> int32 | f32."""
     ptr = torch.tensor([0, 1, 2], device="cuda")
     col = torch.tensor([0, 1], device="cuda")
-    mat = torch.ones((2, 4), dtype=torch.int8, device="cuda")
-    with pytest.raises(ValueError, match="output dtype"):
-        ogn.csr_spmm(ptr, col, None, mat, "sum", output_dtype=torch.float32)
-    with pytest.raises(ValueError, match="output dtype"):
-        ogn.csr_spmm(ptr, col, None, mat.float(), "sum", output_dtype=torch.int32)
+    allowed = {torch.float32: {torch.float32}, torch.float16: {torch.float16, torch.float32},
+               torch.bfloat16: {torch.bfloat16, torch.float32}, torch.int8: {torch.int32, torch.float32}}
+    for src, outs in allowed.items():
+        mat = torch.ones((2, 4), device="cuda").to(src)
+        for out_dtype in (torch.float32, torch.float16, torch.bfloat16, torch.int32):
+            if out_dtype in outs:
+                got = ogn.csr_spmm(ptr, col, None, mat, "sum", output_dtype=out_dtype)
+                assert got.dtype == out_dtype and torch.equal(got.cpu().double(), torch.ones(2, 4).double())
+            else:
+                with pytest.raises(ValueError, match="dtype"):
+                    ogn.csr_spmm(ptr, col, None, mat, "sum", output_dtype=out_dtype)
 
 
 @pytest.mark.parametrize("dtype", DT)
