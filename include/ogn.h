@@ -122,6 +122,27 @@ int ogn_spmm_csr(const void* rowptr, const void* col, int index_dtype, const voi
                  int64_t* arg, int reduce, void* workspace, size_t workspace_bytes,
                  void* stream);
 
+/* ogn_spmm_csr without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The engine
+ * workspace is a library-owned device array of OGN_SPMM_NOALLOC_SCRATCH_BYTES
+ * (128 MiB), one per GPU, held until the process ends; the call uses the
+ * array of the current device (hipGetDevice), which must be the device of
+ * `stream` and of the operands.  A call whose ogn_spmm_csr_workspace_size()
+ * exceeds the maximum returns OGN_EINVAL and launches nothing (config-3 sized
+ * fp32 / bf16 sums fit; min/max at that size do not).  Nothing here calls
+ * hipMalloc / hipFree.  Every call on a GPU shares that GPU's array: calls
+ * that overlap on one GPU (several streams or host threads) race and must
+ * be serialised by the caller.  The array needs no clearing: every entry a
+ * call reads was written earlier in the same call.  Results are bitwise
+ * those of ogn_spmm_csr.
+ */
+#define OGN_SPMM_NOALLOC_SCRATCH_BYTES ((size_t)134217728)
+int ogn_spmm_csr_noalloc(const void* rowptr, const void* col, int index_dtype, const void* value,
+                         int64_t value_width, const void* mat, int in_dtype, int64_t batch,
+                         int64_t m, int64_t n, int64_t k, int64_t nnz, void* out, int out_dtype,
+                         int64_t* arg, int reduce, void* stream);
+
 /* Generalised CSR aggregation (DGL-style spmm / bspmm):
  *   out[b, r, k] = R_{e in row r} msg(mat[b, col[e], k], value[e, (k | 0)])
  * msg: OGN_MSG_MUL (x * w; w = 1 without value), OGN_MSG_ADD (x + w),

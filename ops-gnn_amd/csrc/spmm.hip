@@ -1,13 +1,43 @@
 // CSR SpMM (torch_sparse semantics): the CSR engine in column-gather mode.
 #include "csr_engine.h"
 
+#include <mutex>
 #include <string>
 
 using namespace ogn;
 using namespace ogn::eng;
 
+// Engine workspace of ogn_spmm_csr_noalloc: a file-scope device array, one
+// copy per GPU.  Host code never passes `scratch` itself to a kernel (in
+// host code the name is a stand-in, not a device address); it passes the
+// address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[OGN_SPMM_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 bool is_aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of the current device's `scratch`, looked up once per
+// device (with that device current) and kept.
+int scratch_address(void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(OGN_EHIP, std::string("ogn_spmm_csr_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(OGN_EUNSUPPORTED, "ogn_spmm_csr_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(OGN_EHIP, std::string("ogn_spmm_csr_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return OGN_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -47,6 +77,24 @@ int ogn_spmm_csr_ex(const void* rowptr, const void* col, int index_dtype, const 
     return fail(OGN_EINVAL, "ogn_spmm_csr_ex: unknown semantics");
   return spmm_impl(rowptr, col, index_dtype, value, value_width, mat, in_dtype, batch, m, n, k, nnz, out,
                    out_dtype, arg, reduce, message_op, semantics, workspace, workspace_bytes, stream);
+}
+
+int ogn_spmm_csr_noalloc(const void* rowptr, const void* col, int index_dtype, const void* value,
+                         int64_t value_width, const void* mat, int in_dtype, int64_t batch, int64_t m,
+                         int64_t n, int64_t k, int64_t nnz, void* out, int out_dtype, int64_t* arg,
+                         int reduce, void* stream) {
+  const size_t need = ogn_spmm_csr_workspace_size(m, nnz, k, batch, in_dtype, reduce);
+  if (need > OGN_SPMM_NOALLOC_SCRATCH_BYTES)
+    return fail(OGN_EINVAL, "ogn_spmm_csr_noalloc: this call needs " + std::to_string(need) +
+                                " bytes of scratch, above the maximum of " +
+                                std::to_string(OGN_SPMM_NOALLOC_SCRATCH_BYTES) +
+                                "; use ogn_spmm_csr with a caller workspace");
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != OGN_OK) return rc;
+  return spmm_impl(rowptr, col, index_dtype, value, value_width, mat, in_dtype, batch, m, n, k, nnz, out,
+                   out_dtype, arg, reduce, OGN_MSG_MUL, OGN_SPMM_TORCH_SPARSE, ws, OGN_SPMM_NOALLOC_SCRATCH_BYTES,
+                   stream);
 }
 
 }  // extern "C"

@@ -57,6 +57,8 @@ SIGNATURES = {
     "ogn_spmm_csr_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _int, _int]),
     "ogn_spmm_csr": (_int, [_vp, _vp, _int, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _i64,
                             _vp, _int, _vp, _int, _vp, _sz, _vp]),
+    "ogn_spmm_csr_noalloc": (_int, [_vp, _vp, _int, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _i64,
+                                    _vp, _int, _vp, _int, _vp]),
     "ogn_spmm_csr_ex": (_int, [_vp, _vp, _int, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _i64,
                                _vp, _int, _vp, _int, _int, _int, _vp, _sz, _vp]),
     "ogn_sddmm_csr_workspace_size": (_sz, [_i64, _i64, _int]),
