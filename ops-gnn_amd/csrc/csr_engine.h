@@ -525,7 +525,13 @@ void engine_kernel(Params p) {
         const int32_t oa = xor_shfl<off>(barg[i]);
         bool take;
         if (nanprop) {
-          take = oa != kNone32 && (barg[i] == kNone32 || (ob != ob) || better(ob, best[i], is_min));
+          // a NaN beats any number; between two NaNs, or equal numbers, the
+          // earlier position wins, so every lane ends with the same arg
+          const bool mine_nan = best[i] != best[i], their_nan = ob != ob;
+          take = oa != kNone32 &&
+                 (barg[i] == kNone32 ||
+                  (their_nan ? (!mine_nan || oa < barg[i])
+                             : (!mine_nan && (better(ob, best[i], is_min) || (ob == best[i] && oa < barg[i])))));
         } else if (later) {
           take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
                                    (ob == best[i] && oa > barg[i]));
@@ -760,7 +766,9 @@ void engine_kernel(Params p) {
                                                       : (is_min ? pv >= best[i] : pv <= best[i]);
                   take = !isnan_pv && !blocked;
                 } else {
-                  take = nanprop ? (barg[i] == kNone32 || isnan_pv || better(pv, best[i], is_min))
+                  // NaN-propagating: the first NaN is kept (its position is the arg)
+                  take = nanprop ? (barg[i] == kNone32 || (isnan_pv && best[i] == best[i]) ||
+                                    better(pv, best[i], is_min))
                                  : (!isnan_pv && (barg[i] == kNone32 || better(pv, best[i], is_min) ||
                                                   (later && pv == best[i])));
                 }

@@ -10,9 +10,9 @@ rows give 0).  Every case runs on HIP kernels:
   copy_rhs -> the contiguous-segment engine over the edge rows.
 fp16 accumulates in fp32 (the reference's fp16 kernels accumulate in fp16;
 the fp32 result is the more accurate one and is compared by tolerance).
-Autograd: sum / mean with copy_lhs or mul run backward on the same kernels
-(transposed SpMM for the node operand, SDDMM for the edge operand); other
-combinations raise NotImplementedError when a gradient is required.
+Autograd covers every op x reduce (see _DglSpmm): transposed SpMM for the
+node operand, SDDMM for the edge operand, and the forward's arg edges for
+max / min.
 """
 
 import math
@@ -124,7 +124,10 @@ def _align(lhs, rhs):
     return pad(lhs), pad(rhs)
 
 
-def _forward(request: _SpmmRequest, lhs, rhs) -> torch.Tensor:
+def _forward(request: _SpmmRequest, lhs, rhs, want_arg: bool = False):
+    """(out, arg): out [rows, *feat]; arg [rows, k] int64 (the edge each
+    max / min element came from, E for an empty row; the first NaN edge for
+    a NaN result; the first extremal edge among ties) when `want_arg`."""
     indptr = request.indptr.contiguous()
     indices = request.indices.contiguous()
     rows, edges = indptr.numel() - 1, indices.numel()
@@ -133,11 +136,11 @@ def _forward(request: _SpmmRequest, lhs, rhs) -> torch.Tensor:
         feat = tuple(rhs.shape[1:])
         k = math.prod(feat)
         src3 = rhs.contiguous().reshape(1, edges, k)
-        out3, _ = _native.segment_reduce(src3, indptr.to(torch.int64).reshape(1, -1), rows, reduce,
-                                         _lib.SEM_DGL)
-        return out3.reshape((rows,) + feat)
+        out3, arg3 = _native.segment_reduce(src3, indptr.to(torch.int64).reshape(1, -1), rows, reduce,
+                                            _lib.SEM_DGL, need_arg=want_arg)
+        return out3.reshape((rows,) + feat), (None if arg3 is None else arg3.reshape(rows, k))
     if request.op == "copy_lhs":
-        x, w, wshape = lhs, None, None
+        x, w = lhs, None
         feat = tuple(lhs.shape[1:])
     else:
         x, w = _align(lhs, rhs)
@@ -154,27 +157,52 @@ def _forward(request: _SpmmRequest, lhs, rhs) -> torch.Tensor:
         width = 1 if math.prod(w.shape[1:]) == 1 else k
         value = w.contiguous().reshape(edges, width) if width > 1 else w.contiguous().reshape(edges)
     out = torch.empty((rows, k), dtype=mat.dtype, device=mat.device)
+    arg = torch.empty((rows, k), dtype=torch.int64, device=mat.device) if want_arg else None
     if out.numel():
         ws_bytes = _lib.lib.ogn_spmm_csr_workspace_size(rows, edges, k, 1, _lib.TORCH_TO_OGN[mat.dtype], reduce)
         ws = _lib.workspace(ws_bytes, mat.device)
         rc = _lib.lib.ogn_spmm_csr_ex(
             _lib.dptr(indptr), _lib.dptr(indices), _lib.I64 if indptr.dtype == torch.int64 else _lib.I32,
             _lib.dptr(value), width, _lib.dptr(mat), _lib.TORCH_TO_OGN[mat.dtype], 1, rows, n, k, edges,
-            _lib.dptr(out), _lib.TORCH_TO_OGN[mat.dtype], None, reduce, _MSG[request.op], _lib.SPMM_DGL,
+            _lib.dptr(out), _lib.TORCH_TO_OGN[mat.dtype], _lib.dptr(arg), reduce, _MSG[request.op], _lib.SPMM_DGL,
             _lib.dptr(ws), ws_bytes, _lib.stream_of(mat))
         _lib.check(rc, "spmm")
-    return out.reshape((rows,) + feat)
+    return out.reshape((rows,) + feat), arg
+
+
+def _message_shapes(request: _SpmmRequest, x, w):
+    """(feat, aligned x shape, aligned w shape) of the forward's messages."""
+    if request.op == "copy_rhs":
+        return tuple(w.shape[1:]), None, tuple(w.shape)
+    if request.op == "copy_lhs":
+        return tuple(x.shape[1:]), tuple(x.shape), None
+    xa, wa = _align(x, w)
+    return tuple(torch.broadcast_shapes(xa.shape[1:], wa.shape[1:])), tuple(xa.shape), tuple(wa.shape)
 
 
 class _DglSpmm(torch.autograd.Function):
-    """sum / mean aggregation of copy_lhs or mul messages with gradients."""
+    """Gradients of every op x reduce, matching the reference's torch
+    composition (python/ops_gnn/spmm.py:148-208): message m_e = phi(x[col[e]],
+    w[e]) with phi in {x, w, x + w, x - w, x * w, x / w}, reduced per row.
+
+    sum / mean: each message's gradient is g_e = grad[row(e)] (/ deg).  The
+      node gradient is a transposed SpMM of g with edge weights d phi / dx
+      (none, or w, or 1 / w); the edge gradient is g_e * d phi / dw, formed
+      with the SDDMM kernels (a dot when w has one weight per edge).
+    max / min: only the edge each output element came from (the forward's
+      arg) receives that element's gradient; scattered with index_add.
+    Gradients are summed back over broadcast feature dims; fp32 throughout,
+    cast to the operand dtype at the end.
+    """
 
     @staticmethod
     def forward(ctx, x, w, request):
-        out = _forward(request, x, w)
+        extremum = request.reduce in ("max", "min")
+        out, arg = _forward(request, x, w, want_arg=extremum)
         ctx.request = request
-        ctx.save_for_backward(x, w if w is not None else x)
-        ctx.has_w = w is not None
+        ctx.save_for_backward(x, w, arg)
+        if arg is not None:
+            ctx.mark_non_differentiable(arg)
         return out
 
     @staticmethod
@@ -184,31 +212,86 @@ class _DglSpmm(torch.autograd.Function):
         from .sddmm_csr import sddmm_csr
 
         request = ctx.request
-        x, w_saved = ctx.saved_tensors
-        w = w_saved if ctx.has_w else None
-        indptr = request.indptr.to(torch.int64)
-        indices = request.indices.to(torch.int64)
-        rows, edges = indptr.numel() - 1, indices.numel()
-        g = grad.float().reshape(rows, -1)
-        if request.reduce == "mean":
-            g = g / (indptr[1:] - indptr[:-1]).clamp_min(1).to(torch.float32).unsqueeze(-1)
-        dx = dw = None
-        if ctx.needs_input_grad[0]:
-            perm = torch.argsort(indices, stable=True)
-            colptr = ind2ptr_tensor(indices[perm], x.size(0))
-            row = ptr2ind_tensor(indptr, edges)
-            tw = None
-            if w is not None:
-                tw = w.reshape(edges, -1).float()[perm].contiguous()
-                tw = tw.reshape(edges) if tw.size(1) == 1 else tw
-            dx = _native.spmm_forward(colptr, row[perm].contiguous(), tw, g.contiguous(), 0, torch.float32)[0]
-            dx = dx.reshape(x.shape).to(x.dtype)
-        if ctx.needs_input_grad[1] and w is not None:
-            xf = x.float().reshape(x.size(0), -1).contiguous()
-            width = w.reshape(edges, -1).size(1)
-            dw = sddmm_csr(indptr, indices, g.contiguous(), xf, "dot" if width == 1 else "mul", 0, 2)
-            dw = dw.reshape(w.shape).to(w.dtype)
-        return dx, dw, None
+        x, w, arg = ctx.saved_tensors
+        op = request.op
+        want_x = ctx.needs_input_grad[0] and x is not None
+        want_w = ctx.needs_input_grad[1] and w is not None
+        indptr = request.indptr.to(torch.int64).contiguous()
+        col = request.indices.to(torch.int64).contiguous()
+        rows, edges = indptr.numel() - 1, col.numel()
+        feat, x_shape, w_shape = _message_shapes(request, x, w)
+        k = math.prod(feat)
+        g = grad.float().reshape(rows, k)
+        # operands as the forward saw them: x [N, k]; w [E, width] (width 1 or k)
+        xk = None if x is None else x.float().reshape(x_shape).expand((x.size(0),) + feat).reshape(x.size(0), k)
+        width = 1 if w is None or math.prod(w.shape[1:]) == 1 else k
+        wk = None
+        if w is not None:
+            wk = w.float().reshape(edges, 1) if width == 1 else \
+                w.float().reshape(w_shape).expand((edges,) + feat).reshape(edges, k)
+        dx = torch.zeros_like(xk) if want_x else None
+        dw = torch.zeros((edges, width), dtype=torch.float32, device=g.device) if want_w else None
+        if request.reduce in ("sum", "mean"):
+            if request.reduce == "mean":
+                g = g / indptr.diff().clamp_min(1).to(torch.float32).unsqueeze(-1)
+            g = g.contiguous()
+            if want_x:
+                # d phi / dx per edge: 1 (copy_lhs, add, sub), w (mul), 1 / w (div)
+                scale = wk if op == "mul" else (1.0 / wk if op == "div" else None)
+                sorted_col, perm = torch.sort(col, stable=True)
+                colptr = ind2ptr_tensor(sorted_col, x.size(0))
+                row_t = ptr2ind_tensor(indptr, edges)[perm].contiguous()
+                tw = None
+                if scale is not None:
+                    tw = scale[perm].contiguous()
+                    tw = tw.reshape(edges) if width == 1 else tw
+                dx = _native.spmm_forward(colptr, row_t, tw, g, 0, torch.float32)[0]
+            if want_w:
+                if op in ("copy_rhs", "add", "sub"):
+                    if width == 1:
+                        gw = ptr2ind_tensor(indptr, edges)
+                        dw = g.sum(-1).index_select(0, gw).unsqueeze(-1)
+                    else:
+                        dw = sddmm_csr(indptr, col, g, None, "copy_lhs", 0, 2).reshape(edges, k).float()
+                    if op == "sub":
+                        dw = -dw
+                else:  # mul: g_e * x[col]; div: -g_e * x[col] / w^2
+                    xc = xk.contiguous()
+                    if width == 1:
+                        dw = sddmm_csr(indptr, col, g, xc, "dot", 0, 2).float().unsqueeze(-1)
+                    else:
+                        dw = sddmm_csr(indptr, col, g, xc, "mul", 0, 2).reshape(edges, k).float()
+                    if op == "div":
+                        dw = -dw / (wk * wk)
+        else:
+            hit = arg < edges
+            a = torch.where(hit, arg, torch.zeros_like(arg))
+            ge = torch.where(hit, g, torch.zeros_like(g))
+            feature = torch.arange(k, device=g.device).expand(rows, k)
+            wv = None if wk is None else (wk[a, 0] if width == 1 else wk[a, feature])
+            src = col[a] if xk is not None else None
+            if want_x:
+                dphi_dx = ge if op in ("copy_lhs", "add", "sub") else (ge * wv if op == "mul" else ge / wv)
+                dx.view(-1).index_add_(0, (src * k + feature).reshape(-1), dphi_dx.reshape(-1))
+            if want_w:
+                if op in ("copy_rhs", "add"):
+                    dphi_dw = ge
+                elif op == "sub":
+                    dphi_dw = -ge
+                else:
+                    xv = xk[src, feature]
+                    dphi_dw = ge * xv if op == "mul" else -ge * xv / (wv * wv)
+                slot = a if width == 1 else a * k + feature
+                dw.view(-1).index_add_(0, slot.reshape(-1), dphi_dw.reshape(-1))
+        gx = gw_out = None
+        if want_x:
+            gx = dx.reshape((x.size(0),) + feat).sum_to_size(x_shape).reshape(x.shape).to(x.dtype)
+        if want_w:
+            if width == 1:
+                gw_out = dw.reshape(w.shape).to(w.dtype)
+            else:
+                gw_out = dw.reshape((edges,) + feat).sum_to_size(w_shape).reshape(w.shape).to(w.dtype)
+        return gx, gw_out, None
 
 
 def _spmm(request: _SpmmRequest) -> torch.Tensor:
@@ -225,13 +308,9 @@ def _spmm(request: _SpmmRequest) -> torch.Tensor:
     _validate(request, lhs, edge)
     grad_required = torch.is_grad_enabled() and any(v is not None and v.requires_grad for v in (lhs, edge))
     if grad_required:
-        if request.reduce in ("sum", "mean") and request.op in ("copy_lhs", "mul"):
-            result = _DglSpmm.apply(lhs, edge, request)
-        else:
-            raise NotImplementedError(f"{api}: gradients of op={request.op}, reduce={request.reduce} are not "
-                                      "implemented on the GPU path")
+        result = _DglSpmm.apply(lhs, edge, request)
     else:
-        result = _forward(request, lhs, edge)
+        result = _forward(request, lhs, edge)[0]
     out = request.out
     if out is None:
         return result

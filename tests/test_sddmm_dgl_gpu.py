@@ -213,3 +213,88 @@ def test_dgl_backward(ogn, reduce, op):
     np.testing.assert_allclose(x.grad.cpu().numpy(), dx.numpy(), rtol=1e-4, atol=1e-4)
     if w is not None:
         np.testing.assert_allclose(w.grad.cpu().numpy(), dv.numpy(), rtol=1e-4, atol=1e-4)
+
+
+def _torch_composition(ptr, col, x, w, op, reduce):
+    """The reference's torch composition (python/ops_gnn/spmm.py:148-208) in
+    float64 on the CPU: gather, message op with rank alignment, then
+    index_add (sum / mean) or per-row max / min over dim 0."""
+    m = ptr.numel() - 1
+    gathered = None if x is None else x.index_select(0, col)
+    if op == "copy_lhs":
+        msg = gathered
+    elif op == "copy_rhs":
+        msg = w
+    else:
+        rank = max(gathered.dim(), w.dim()) - 1
+        pad = lambda v: v.reshape((v.shape[0],) + (1,) * (rank - v.dim() + 1) + tuple(v.shape[1:]))
+        a, b = pad(gathered), pad(w)
+        msg = {"add": a + b, "sub": a - b, "mul": a * b, "div": a / b}[op]
+    counts = ptr.diff()
+    if reduce in ("sum", "mean"):
+        rows = torch.repeat_interleave(torch.arange(m), counts)
+        out = msg.new_zeros((m,) + tuple(msg.shape[1:])).index_add(0, rows, msg)
+        if reduce == "mean":
+            out = out / counts.clamp(min=1).to(out.dtype).reshape((m,) + (1,) * (msg.dim() - 1))
+        return out
+    parts = []
+    for r in range(m):
+        a, b = int(ptr[r]), int(ptr[r + 1])
+        if a == b:
+            parts.append(msg.new_zeros(msg.shape[1:]))
+        else:
+            seg = msg[a:b]
+            parts.append(seg.max(dim=0).values if reduce == "max" else seg.min(dim=0).values)
+    return torch.stack(parts)
+
+
+_GRAD_CASES = [
+    # (op, x feature shape, w feature shape, batched)
+    ("copy_lhs", (6,), None, False),
+    ("copy_rhs", None, (6,), False),
+    ("add", (6,), (6,), False),
+    ("sub", (6,), (1,), False),
+    ("mul", (6,), (), False),
+    ("div", (6,), (6,), False),
+    ("mul", (3, 4), (3, 1), True),
+    ("add", (1, 4), (3, 4), True),
+    ("div", (3, 4), (), True),
+    ("copy_lhs", (2, 5), None, True),
+]
+
+
+@pytest.mark.parametrize("op,xs,ws,batched", _GRAD_CASES)
+@pytest.mark.parametrize("reduce", ["sum", "mean", "max", "min"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_dgl_gradients_every_op_and_reduce(ogn, op, xs, ws, batched, reduce, dtype):
+    """spmm / bspmm gradients for every message op and reduction, against
+    float64 autograd through the reference's composition (no ties: random
+    continuous data, divisors kept away from zero)."""
+    ptr, col, rng = _csr(90, 70, 5, seed=17, hub=60)
+    e = col.numel()
+    x64 = None if xs is None else torch.from_numpy(rng.standard_normal((70,) + xs))
+    w64 = None if ws is None else torch.from_numpy(rng.uniform(0.5, 2.0, (e,) + ws)
+                                                   * rng.choice([-1.0, 1.0], (e,) + ws))
+    if dtype == torch.float16:  # compare on the exact fp16 inputs
+        x64 = None if x64 is None else x64.half().double()
+        w64 = None if w64 is None else w64.half().double()
+    leaves = [t.clone().requires_grad_(True) for t in (x64, w64) if t is not None]
+    x_ref = leaves[0] if x64 is not None else None
+    w_ref = leaves[-1] if w64 is not None else None
+    ref = _torch_composition(ptr, col, x_ref, w_ref, op, reduce)
+    g = torch.from_numpy(rng.standard_normal(tuple(ref.shape)))
+    ref.backward(g)
+    xg = None if x64 is None else x64.to(dtype).cuda().requires_grad_(True)
+    wg = None if w64 is None else w64.to(dtype).cuda().requires_grad_(True)
+    fn = ogn.bspmm if batched else ogn.spmm
+    if op == "copy_rhs":
+        out = fn(ptr.cuda(), col.cuda(), None, op=op, reduce=reduce, rhs=wg)
+    else:
+        out = fn(ptr.cuda(), col.cuda(), xg, op=op, reduce=reduce, rhs=wg)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(out.double().cpu(), ref.detach(), rtol=tol, atol=tol)
+    out.backward(g.to(dtype).cuda())
+    if xg is not None:
+        torch.testing.assert_close(xg.grad.double().cpu(), x_ref.grad, rtol=tol, atol=tol)
+    if wg is not None:
+        torch.testing.assert_close(wg.grad.double().cpu(), w_ref.grad, rtol=tol, atol=tol)
