@@ -279,13 +279,18 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
  * [segments + 1]).  out = exp(x - clamp(m)) / s or (x - clamp(m)) - log(s)
  * with (m, s) as ogn_segment_group_stats; a row holding +inf is NaN
  * throughout.  Positions outside [indptr[0], indptr[segments]) are not
- * written.  16, 32 or 64 lanes per row (by the average row length): meant
- * for rows of >= ~64 positions on average.  src and out 16-byte aligned, and length * element size a
- * multiple of 16 when batch > 1.  No workspace.  Fuses the sorted-index
+ * written.  One wavefront per row of up to 2048 (fp16 / bf16) or 1024 (fp32)
+ * positions, a 256-thread block per longer row: meant for rows of >= ~64
+ * positions on average.  src and out 16-byte aligned, and length * element
+ * size a multiple of 16 when batch > 1.  Workspace (256-byte aligned, its
+ * contents need no initialisation): the long-row list,
+ * ogn_segment_group_softmax_workspace_size() bytes.  Fuses the sorted-index
  * forward phases of scatter_softmax / scatter_log_softmax (reference
  * csrc/npu/scatter_softmax/common/grouped_softmax_shared.h:178-209). */
+size_t ogn_segment_group_softmax_workspace_size(int64_t batch, int64_t length, int64_t segments, int dtype);
 int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
-                              int64_t segments, void* out, int log_softmax, void* stream);
+                              int64_t segments, void* out, int log_softmax, void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /* ------------------------------------------------------------------ unsorted scatter
  * torch_scatter scatter with an arbitrary int64 index (same rules as

@@ -4,6 +4,7 @@
 #include "csr_engine.h"
 #include "typed.h"
 
+#include <cstdlib>
 #include <string>
 
 using namespace ogn;
@@ -148,66 +149,401 @@ __global__ __launch_bounds__(256) void row_stats_k1_kernel(const int64_t* __rest
   }
 }
 
-// Fused softmax / log_softmax of one-feature rows: the statistics as above,
-// then a second pass over the row (just read, so served by the caches) that
-// writes exp(x - clamp(m)) / s or (x - clamp(m)) - log(s); a row holding
-// +inf gives NaN throughout (torch.softmax).  Packets shared with a
-// neighbouring row are written element by element.
+// Per-row constants of the softmax outputs: inv = 1 / s and ls = ln s from
+// the hardware reciprocal and log2 (about 1 ulp each; an output is
+// e * inv or (x - m) - ls, well inside the fp32 tolerance), both NaN for a
+// row holding +inf, so that every output of such a row is NaN.
+__device__ __forceinline__ void softmax_row_constants(float m, float s, float& inv, float& ls) {
+  const bool poisoned = m == __builtin_inff();
+  inv = poisoned ? __builtin_nanf("") : __builtin_amdgcn_rcpf(s);
+  ls = poisoned ? __builtin_nanf("") : __builtin_amdgcn_logf(s) * 0.693147180559945309f;
+}
+
+// 64-lane reduction for the row kernels: four DPP steps inside each 16-lane
+// row (quad_perm xor 1, quad_perm xor 2, half-row mirror, row mirror), after
+// which every lane of a row holds the row's result, then the four row
+// results are read as uniform values and combined.  Every lane returns the
+// same bits (each step combines the same two operands on both partners).
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce64(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  v = op(v, dpp(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  v = op(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+  const int b = __float_as_int(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+  return op(op(r0, r1), op(r2, r3));
+}
+
+// Softmax / log_softmax of one one-feature row held in registers: the row
+// spans at most 64 * U aligned 16-byte packets; lane l holds packets l,
+// l + 64, ...  fetch_row_packets issues the U loads (all in flight at once;
+// packets past the row read as zero), finish_row_packets masks positions
+// outside [rs, re) to -inf and computes the max, the sum of exponentials and
+// the outputs from registers: one read and one exponential per position.
+// A row holding +inf gives NaN throughout (torch.softmax).
+// Every lane issues its U loads unconditionally, so that all of them are in
+// flight before the first is used (a load under a branch, merged with a
+// default value, makes the compiler wait for it on the spot).  A packet
+// outside the row, or not wholly inside the buffer, re-reads a packet the
+// row already reads (addresses stay in bounds; its values are masked or
+// reloaded element by element in finish_row_packets).
+template <int DT>
+__device__ __forceinline__ int64_t packet_address(int64_t q, int64_t q0, int64_t re, int64_t length) {
+  constexpr int V = Elem<DT>::VEC;
+  const int64_t last_full = (length - V) / V * V;  // length >= V
+  return q < re && q + V <= length ? q : std::min<int64_t>(q0, last_full);
+}
+
+template <int DT, int U>
+__device__ __forceinline__ void fetch_row_packets(const typename Elem<DT>::S* __restrict__ row, int64_t rs,
+                                                  int64_t re, int64_t length, uint4* raw) {
+  constexpr int V = Elem<DT>::VEC;
+  if (length < V) return;  // no whole packet: finish_row_packets loads elements
+  const int64_t q0 = rs / V * V;
+  const int lane = (int)lane_id();
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t q = q0 + (int64_t)(u * kWave + lane) * V;
+    raw[u] = load16(row + packet_address<DT>(q, q0, re, length));
+  }
+}
+
+template <int DT, int U>
+__device__ __forceinline__ void finish_row_packets(const typename Elem<DT>::S* __restrict__ row,
+                                                   void* __restrict__ out, int64_t obase, int64_t rs, int64_t re,
+                                                   int64_t length, int log_mode, const uint4* raw) {
+  using E = Elem<DT>;
+  constexpr int V = E::VEC;
+  const int64_t q0 = rs / V * V;
+  const int lane = (int)lane_id();
+  const uint32_t n = (uint32_t)(re - rs);
+  float x[U][V];
+  float pm = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t q = q0 + (int64_t)(u * kWave + lane) * V;
+    if (q < re && q + V > length) {  // the buffer's last, partial packet
+#pragma unroll
+      for (int i = 0; i < V; ++i) x[u][i] = q + i < length ? E::load1(row, q + i) : 0.f;
+    } else {
+      E::unpack(raw[u], x[u]);
+    }
+    const int32_t d = (int32_t)(q - rs);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      x[u][i] = (uint32_t)(d + i) < n ? x[u][i] : -__builtin_inff();
+      pm = fmaxf(pm, x[u][i]);  // NaN-ignoring
+    }
+  }
+  const float m = wave_reduce64<true>(pm);
+  const float cm = clampf_max(m);
+  float ps = 0.f;
+  if (log_mode) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < V; ++i) ps += fast_exp(x[u][i] - cm);
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        x[u][i] = fast_exp(x[u][i] - cm);
+        ps += x[u][i];
+      }
+  }
+  const float s = wave_reduce64<false>(ps);
+  float inv, ls;
+  softmax_row_constants(m, s, inv, ls);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t q = q0 + (int64_t)(u * kWave + lane) * V;
+    if (q >= re) continue;
+    const int32_t d = (int32_t)(q - rs);
+    float v[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = log_mode ? (x[u][i] - cm) - ls : x[u][i] * inv;
+    if (d >= 0 && (uint32_t)(d + V) <= n) {
+      store_floats<V, true>(out, DT, obase + q, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        if ((uint32_t)(d + i) < n) store_floats<1>(out, DT, obase + q + i, &v[i]);
+    }
+  }
+}
+
+template <int DT, int U>
+__device__ __forceinline__ void softmax_row_in_registers(const typename Elem<DT>::S* __restrict__ row,
+                                                         void* __restrict__ out, int64_t obase, int64_t rs,
+                                                         int64_t re, int64_t length, int log_mode) {
+  uint4 raw[U];
+  fetch_row_packets<DT, U>(row, rs, re, length, raw);
+  finish_row_packets<DT, U>(row, out, obase, rs, re, length, log_mode, raw);
+}
+
+// Rows of up to kWaveRowPackets packets: one wavefront each, in registers.
+// Longer rows (the tail of a lognormal or power-law degree distribution) are
+// listed by that kernel and done by row_softmax_long_kernel, a block per row.
+constexpr int64_t kWaveRowPackets = 4 * kWave;
+
+template <int DT>
+__device__ __forceinline__ int64_t row_packets(int64_t rs, int64_t re) {
+  constexpr int V = Elem<DT>::VEC;
+  return re > rs ? (re - rs / V * V + V - 1) / V : 0;
+}
+
+// Workspace of ogn_segment_group_softmax: a long-row counter, then the list
+// of long rows (b * segments + r), at most one per kWaveRowPackets * VEC
+// positions of each batch.
+struct LongRowList {
+  unsigned long long* count;
+  int64_t* rows;
+};
+constexpr size_t kListHeader = 256;
+inline int64_t long_row_capacity(int64_t batch, int64_t length, int64_t segments, int vec) {
+  return batch * std::min<int64_t>(segments, length / (kWaveRowPackets * vec) + 1);
+}
+
+__global__ void zero_u64_kernel(unsigned long long* p) { *p = 0; }
+
+// One row per wavefront (4 per block): rows of up to 64 * 4 packets in
+// registers (tier chosen by length, wave-uniform); a longer row is appended
+// to the long-row list.
 template <int DT>
 __global__ __launch_bounds__(256) void row_softmax_k1_kernel(const int64_t* __restrict__ ptr,
                                                              const void* __restrict__ src, int64_t length,
-                                                             int64_t segments, void* __restrict__ out, int log_mode) {
+                                                             int64_t segments, void* __restrict__ out, int log_mode,
+                                                             LongRowList list) {
   using E = Elem<DT>;
-  constexpr int V = E::VEC;
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= segments) return;
   const int64_t b = blockIdx.y;
   const int64_t rs = std::max<int64_t>(ptr[r], 0);
   const int64_t re = std::min<int64_t>(ptr[r + 1], length);
+  const int64_t packets = row_packets<DT>(rs, re);
+  if (packets == 0) return;
   const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
-  float m, sacc;
-  row_lse_k1<DT>(row, rs, re, length, m, sacc);
-  const float cm = clampf_max(m);
-  const float ls = logf(sacc);
-  const float inv = 1.f / sacc;
-  const bool poisoned = m == __builtin_inff();
-#pragma unroll 2
-  for (int64_t q = rs / V * V + (int64_t)lane_id() * V; q < re; q += (int64_t)kWave * V) {
-    float x[V], v[V];
-    load_packet<DT>(row, q, rs, re, length, x);
+  const int64_t obase = b * length;
+  if (packets <= kWave) return softmax_row_in_registers<DT, 1>(row, out, obase, rs, re, length, log_mode);
+  if (packets <= 2 * kWave) return softmax_row_in_registers<DT, 2>(row, out, obase, rs, re, length, log_mode);
+  if (packets <= 3 * kWave) return softmax_row_in_registers<DT, 3>(row, out, obase, rs, re, length, log_mode);
+  if (packets <= 4 * kWave) return softmax_row_in_registers<DT, 4>(row, out, obase, rs, re, length, log_mode);
+  if (lane_id() == 0) list.rows[atomicAdd(list.count, 1ull)] = b * segments + r;
+}
+
+// Reduction over a 256-thread block: wave_reduce64, then the 4 wave
+// results combined in wave order from LDS (every thread gets the same bits).
+template <bool MAX>
+__device__ __forceinline__ float block_reduce256(float v, float* red) {
+  v = wave_reduce64<MAX>(v);
+  if (lane_id() == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = MAX ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return r;
+}
+
+// One long row in registers over a 256-thread block: UB packets per thread.
+template <int DT, int UB>
+__device__ __forceinline__ void block_row_in_registers(const typename Elem<DT>::S* __restrict__ row,
+                                                       void* __restrict__ out, int64_t obase, int64_t rs, int64_t re,
+                                                       int64_t length, int log_mode, float* red) {
+  using E = Elem<DT>;
+  constexpr int V = E::VEC;
+  constexpr int T = 256;
+  const int t = (int)threadIdx.x;
+  const int64_t q0 = rs / V * V;
+  const uint32_t n = (uint32_t)(re - rs);
+    uint4 raw[UB];
 #pragma unroll
-    for (int i = 0; i < V; ++i)
-      v[i] = log_mode ? (x[i] - cm) - ls : fast_exp(x[i] - cm) * inv;
-    if (poisoned) {
+    for (int u = 0; u < UB; ++u)
+      raw[u] = load16(row + packet_address<DT>(q0 + (int64_t)(u * T + t) * V, q0, re, length));
+    float x[UB][V];
+    float pm = -__builtin_inff();
 #pragma unroll
-      for (int i = 0; i < V; ++i) v[i] = __builtin_nanf("");
+    for (int u = 0; u < UB; ++u) {
+      const int64_t q = q0 + (int64_t)(u * T + t) * V;
+      if (q < re && q + V > length) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) x[u][i] = q + i < length ? E::load1(row, q + i) : 0.f;
+      } else {
+        E::unpack(raw[u], x[u]);
+      }
+      const int32_t d = (int32_t)(q - rs);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        x[u][i] = (uint32_t)(d + i) < n ? x[u][i] : -__builtin_inff();
+        pm = fmaxf(pm, x[u][i]);
+      }
     }
-    const int64_t o = b * length + q;
-    if (q >= rs && q + V <= re) {
-      store_floats<V, true>(out, DT, o, v);
-    } else {
+    const float m = block_reduce256<true>(pm, red);
+    const float cm = clampf_max(m);
+    float ps = 0.f;
 #pragma unroll
-      for (int i = 0; i < V; ++i)
-        if (q + i >= rs && q + i < re) store_floats<1>(out, DT, o + i, &v[i]);
+    for (int u = 0; u < UB; ++u)
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float e = fast_exp(x[u][i] - cm);
+        ps += e;
+        if (!log_mode) x[u][i] = e;
+      }
+    const float s = block_reduce256<false>(ps, red);
+    float inv, ls;
+    softmax_row_constants(m, s, inv, ls);
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int64_t q = q0 + (int64_t)(u * T + t) * V;
+      if (q >= re) continue;
+      const int32_t d = (int32_t)(q - rs);
+      float v[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[i] = log_mode ? (x[u][i] - cm) - ls : x[u][i] * inv;
+      if (d >= 0 && (uint32_t)(d + V) <= n) {
+        store_floats<V, true>(out, DT, obase + q, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          if ((uint32_t)(d + i) < n) store_floats<1>(out, DT, obase + q + i, &v[i]);
+      }
+    }
+}
+
+// The listed long rows, a 256-thread block per row (blocks stride over the
+// list).  Rows of up to 256 * 8 packets (16 384 fp16 positions) stay in
+// registers (8 loads in flight per thread); longer rows take two passes over
+// chunks of 256 * 8 packets (log-sum-exp statistics, then the outputs), each
+// chunk's 8 loads per thread issued together.
+template <int DT>
+__global__ __launch_bounds__(256) void row_softmax_long_kernel(const int64_t* __restrict__ ptr,
+                                                               const void* __restrict__ src, int64_t length,
+                                                               int64_t segments, void* __restrict__ out,
+                                                               int log_mode, LongRowList list) {
+  using E = Elem<DT>;
+  constexpr int V = E::VEC;
+  constexpr int UB = 8;
+  constexpr int T = 256;
+  __shared__ float red[4];
+  const int t = (int)threadIdx.x;
+  const int64_t count = (int64_t)*list.count;
+  for (int64_t item = blockIdx.x; item < count; item += gridDim.x) {
+    const int64_t code = list.rows[item];
+    const int64_t b = code / segments, r = code - b * segments;
+    const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
+    const int64_t obase = b * length;
+    const int64_t rs = std::max<int64_t>(ptr[r], 0);
+    const int64_t re = std::min<int64_t>(ptr[r + 1], length);
+    const int64_t q0 = rs / V * V;
+    const uint32_t n = (uint32_t)(re - rs);
+    const int64_t pk = row_packets<DT>(rs, re);
+    if (pk <= 2 * T) {
+      block_row_in_registers<DT, 2>(row, out, obase, rs, re, length, log_mode, red);
+    } else if (pk <= 4 * T) {
+      block_row_in_registers<DT, 4>(row, out, obase, rs, re, length, log_mode, red);
+    } else if (pk <= (int64_t)UB * T) {
+      block_row_in_registers<DT, UB>(row, out, obase, rs, re, length, log_mode, red);
+    } else {
+      // statistics: per-thread online (m, s) over chunks, then block max and
+      // rescaled sum
+      constexpr int64_t kChunk = (int64_t)UB * T * V;
+      float m = -__builtin_inff(), sacc = 0.f;
+      for (int64_t c0 = q0; c0 < re; c0 += kChunk) {
+        uint4 raw[UB];
+#pragma unroll
+        for (int u = 0; u < UB; ++u)
+          raw[u] = load16(row + packet_address<DT>(c0 + (int64_t)(u * T + t) * V, q0, re, length));
+        float pm = m;
+        float x[UB][V];
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+          const int64_t q = c0 + (int64_t)(u * T + t) * V;
+          if (q < re && q + V > length) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) x[u][i] = q + i < length ? E::load1(row, q + i) : 0.f;
+          } else {
+            E::unpack(raw[u], x[u]);
+          }
+          const int64_t d = q - rs;
+#pragma unroll
+          for (int i = 0; i < V; ++i) {
+            x[u][i] = (uint64_t)(d + i) < (uint64_t)n ? x[u][i] : -__builtin_inff();
+            pm = fmaxf(pm, x[u][i]);
+          }
+        }
+        const float cn = clampf_max(pm);
+        float acc = sacc * fast_exp(clampf_max(m) - cn);
+#pragma unroll
+        for (int u = 0; u < UB; ++u)
+#pragma unroll
+          for (int i = 0; i < V; ++i) acc += fast_exp(x[u][i] - cn);
+        m = pm;
+        sacc = acc;
+      }
+      const float gm = block_reduce256<true>(m, red);
+      const float sv = sacc == 0.f ? 0.f : sacc * fast_exp(clampf_max(m) - clampf_max(gm));
+      const float s = block_reduce256<false>(sv, red);
+      const float cm = clampf_max(gm);
+      float inv, ls;
+      softmax_row_constants(gm, s, inv, ls);
+      for (int64_t c0 = q0; c0 < re; c0 += kChunk) {
+        uint4 raw[UB];
+#pragma unroll
+        for (int u = 0; u < UB; ++u)
+          raw[u] = load16(row + packet_address<DT>(c0 + (int64_t)(u * T + t) * V, q0, re, length));
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+          const int64_t q = c0 + (int64_t)(u * T + t) * V;
+          if (q >= re) continue;
+          float x[V], v[V];
+          if (q + V > length) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) x[i] = q + i < length ? E::load1(row, q + i) : 0.f;
+          } else {
+            E::unpack(raw[u], x);
+          }
+#pragma unroll
+          for (int i = 0; i < V; ++i) v[i] = log_mode ? (x[i] - cm) - ls : fast_exp(x[i] - cm) * inv;
+          const int64_t d = q - rs;
+          if (d >= 0 && d + V <= (int64_t)n) {
+            store_floats<V, true>(out, DT, obase + q, v);
+          } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+              if ((uint64_t)(d + i) < (uint64_t)n) store_floats<1>(out, DT, obase + q + i, &v[i]);
+          }
+        }
+      }
     }
   }
 }
 
 template <int DT>
-void launch_row_kernel(bool softmax, dim3 grid, hipStream_t st, const int64_t* ptr, const void* src, int64_t length,
-                       int64_t segments, float* m, float* s, void* out, int lm) {
-  if (softmax)
-    hipLaunchKernelGGL(row_softmax_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, out, lm);
-  else
-    hipLaunchKernelGGL(row_stats_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, m, s);
+void launch_softmax_rows(dim3 grid, hipStream_t st, const int64_t* ptr, const void* src, int64_t length,
+                         int64_t segments, void* out, int lm, LongRowList list, int64_t capacity) {
+  hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(1), 0, st, list.count);
+  hipLaunchKernelGGL(row_softmax_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, out, lm, list);
+  const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(capacity, 4096));
+  hipLaunchKernelGGL(row_softmax_long_kernel<DT>, dim3(blocks), dim3(256), 0, st, ptr, src, length, segments, out,
+                     lm, list);
 }
 
-void launch_rows(bool softmax, int dtype, int64_t batch, hipStream_t st, const int64_t* ptr, const void* src,
-                 int64_t length, int64_t segments, float* m, float* s, void* out, int lm) {
+void launch_stats_rows(int dtype, int64_t batch, hipStream_t st, const int64_t* ptr, const void* src, int64_t length,
+                       int64_t segments, float* m, float* s) {
   const dim3 grid((unsigned)((segments + 3) / 4), (unsigned)batch);
-  if (dtype == OGN_F32) launch_row_kernel<OGN_F32>(softmax, grid, st, ptr, src, length, segments, m, s, out, lm);
-  else if (dtype == OGN_F16) launch_row_kernel<OGN_F16>(softmax, grid, st, ptr, src, length, segments, m, s, out, lm);
-  else launch_row_kernel<OGN_BF16>(softmax, grid, st, ptr, src, length, segments, m, s, out, lm);
+  if (dtype == OGN_F32)
+    hipLaunchKernelGGL(row_stats_k1_kernel<OGN_F32>, grid, dim3(256), 0, st, ptr, src, length, segments, m, s);
+  else if (dtype == OGN_F16)
+    hipLaunchKernelGGL(row_stats_k1_kernel<OGN_F16>, grid, dim3(256), 0, st, ptr, src, length, segments, m, s);
+  else
+    hipLaunchKernelGGL(row_stats_k1_kernel<OGN_BF16>, grid, dim3(256), 0, st, ptr, src, length, segments, m, s);
 }
 
 }  // namespace
@@ -308,7 +644,7 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
       batch <= 65535) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     TimedLaunch t("segment_stats_main", st);
-    launch_rows(false, dtype, batch, st, indptr, src, length, segments, m_out, s_out, nullptr, 0);
+    launch_stats_rows(dtype, batch, st, indptr, src, length, segments, m_out, s_out);
     return check_launch("ogn_segment_group_stats");
   }
   const bool aligned = is_aligned(src, 16) && is_aligned(m_out, 16);
@@ -332,8 +668,15 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
              static_cast<hipStream_t>(stream), "segment_stats");
 }
 
+size_t ogn_segment_group_softmax_workspace_size(int64_t batch, int64_t length, int64_t segments, int dtype) {
+  if (batch <= 0 || length < 0 || segments < 0) return 0;
+  const int vec = 16 / dtype_size(dtype);
+  return kListHeader + sizeof(int64_t) * (size_t)long_row_capacity(batch, length, segments, vec);
+}
+
 int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
-                              int64_t segments, void* out, int log_softmax, void* stream) {
+                              int64_t segments, void* out, int log_softmax, void* workspace, size_t workspace_bytes,
+                              void* stream) {
   if (batch < 0 || length < 0 || segments < 0) return fail(OGN_EINVAL, "ogn_segment_group_softmax: negative size");
   if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
     return fail(OGN_EUNSUPPORTED, "ogn_segment_group_softmax: src dtype must be float32, float16 or bfloat16");
@@ -342,9 +685,21 @@ int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype,
   if (!is_aligned(src, 16) || !is_aligned(out, 16) || (batch > 1 && (length * dtype_size(dtype)) % 16 != 0))
     return fail(OGN_EINVAL, "ogn_segment_group_softmax: src / out rows must be 16-byte aligned");
   if (batch > 65535) return fail(OGN_EUNSUPPORTED, "ogn_segment_group_softmax: batch > 65535");
+  const size_t need = ogn_segment_group_softmax_workspace_size(batch, length, segments, dtype);
+  if (!workspace || workspace_bytes < need || !is_aligned(workspace, 256))
+    return fail(OGN_EINVAL, "ogn_segment_group_softmax: workspace too small or not 256-byte aligned (need " +
+                                std::to_string(need) + " bytes)");
+  const int vec = 16 / dtype_size(dtype);
+  LongRowList list{static_cast<unsigned long long*>(workspace),
+                   reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + kListHeader)};
+  const int64_t capacity = long_row_capacity(batch, length, segments, vec);
   hipStream_t st = static_cast<hipStream_t>(stream);
   TimedLaunch t("segment_softmax", st);
-  launch_rows(true, dtype, batch, st, indptr, src, length, segments, nullptr, nullptr, out, log_softmax ? 1 : 0);
+  const dim3 grid((unsigned)((segments + 3) / 4), (unsigned)batch);
+  const int lm = log_softmax ? 1 : 0;
+  if (dtype == OGN_F32) launch_softmax_rows<OGN_F32>(grid, st, indptr, src, length, segments, out, lm, list, capacity);
+  else if (dtype == OGN_F16) launch_softmax_rows<OGN_F16>(grid, st, indptr, src, length, segments, out, lm, list, capacity);
+  else launch_softmax_rows<OGN_BF16>(grid, st, indptr, src, length, segments, out, lm, list, capacity);
   return check_launch("ogn_segment_group_softmax");
 }
 

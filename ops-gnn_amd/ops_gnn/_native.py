@@ -264,8 +264,11 @@ def group_softmax_rows(src3: torch.Tensor, ptr: torch.Tensor, groups: int, log_s
     out = torch.empty_like(src3)
     if out.numel() == 0:
         return out
-    rc = lib.ogn_segment_group_softmax(dptr(ptr), dptr(src3), _lib.TORCH_TO_OGN[src3.dtype], b, length, groups,
-                                       dptr(out), 1 if log_softmax else 0, stream_of(src3))
+    code = _lib.TORCH_TO_OGN[src3.dtype]
+    ws_bytes = lib.ogn_segment_group_softmax_workspace_size(b, length, groups, code)
+    ws = _lib.workspace(ws_bytes, src3.device)
+    rc = lib.ogn_segment_group_softmax(dptr(ptr), dptr(src3), code, b, length, groups, dptr(out),
+                                       1 if log_softmax else 0, dptr(ws), ws_bytes, stream_of(src3))
     check(rc, "grouped softmax")
     return out
 

@@ -207,6 +207,23 @@ def test_grouped_softmax_long_edge_rows(ogn, oracle, dtype, mode, before, mean_l
     _softmax_check(ogn, oracle, src, torch.from_numpy(idx), 1, 300, mode, SOFT_TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax"])
+def test_grouped_softmax_register_row_sizes(ogn, oracle, dtype, mode):
+    # one-feature rows whose packet counts straddle every register tier of
+    # the fused row kernel (64 / 128 / 256 / 512 packets of 4 or 8 positions)
+    # and the two-pass path beyond, at unaligned starts
+    v = 8 if dtype != torch.float32 else 4
+    sizes = [1, v - 1, v, v + 1, 64 * v - 1, 64 * v, 64 * v + 1, 128 * v + 3, 256 * v, 256 * v + 5,
+             512 * v - 2, 512 * v, 512 * v + 1, 1500 * v, 3]
+    rng = np.random.default_rng(54)
+    deg = np.array(sizes, dtype=np.int64)
+    idx = np.repeat(np.arange(deg.size), deg)
+    x = (rng.standard_normal((2, idx.size)) * 5).astype(np.float32)
+    src = torch.from_numpy(x).to(dtype)
+    _softmax_check(ogn, oracle, src, torch.from_numpy(idx), 1, deg.size, mode, SOFT_TOL[dtype])
+
+
 @pytest.mark.parametrize("sorted_index", [True, False])
 def test_grouped_softmax_special_values(ogn, oracle, sorted_index):
     src = torch.tensor([INF, 1.0, -INF, 2.0, NAN, 0.0, -INF, -INF])
