@@ -79,8 +79,74 @@ def _finish(result3, out, shape):
     return out
 
 
+# ------------------------------------------------------------------ A2 (arch22) semantics
+# The reference's Atlas A2 build binds segment_csr / segment_coo with other
+# forward rules than the Ascend 950 build (docs/en/api_reference.md:1778-1795,
+# goldens test/segment_csr/arch22/golden.py:68-153 and
+# test/segment_coo/arch22/golden.py:63-160).  semantics="a2" selects them.
+# They are derived on the GPU from the first-tie, NaN-ignoring segment
+# kernels (SEM_SEGMENT_CSR) plus elementwise passes:
+#   * extrema update only on strict improvement, from the supplied out
+#     (segment_coo) or from the work dtype's finite identity; a result still
+#     equal to the identity is the identity (segment_csr) or zero (segment_coo
+#     without out);
+#   * the arg of an element without an improvement carries the last
+#     improving position of the same feature across the flattened
+#     (batch, segment) order, starting from 0; empty segments give the
+#     length sentinel;
+#   * segment_coo seeds sum / mean with out, the segment holding position 0 of
+#     a batch reads out[batch, 0], and its mean divides by the count narrowed
+#     to the source dtype (zero when that is zero); segment_csr's fp16 / bf16
+#     mean narrows the sum before the division.
+_SEMANTICS = ("arch35", "a2")
+
+
+def _check_semantics(semantics: str) -> None:
+    if semantics not in _SEMANTICS:
+        raise ValueError(f"semantics must be one of {_SEMANTICS}, got {semantics!r}")
+
+
+def _work_dtype(dtype):
+    return torch.float32 if dtype in (torch.float16, torch.bfloat16) else dtype
+
+
+def _identity(dtype, reduce):
+    work = _work_dtype(dtype)
+    info = torch.finfo(work) if work.is_floating_point else torch.iinfo(work)
+    return info.max if reduce == "min" else info.min
+
+
+def _strictly_better(v, ref, reduce):
+    """v strictly improves on ref (NaN never does), compared in the work dtype."""
+    work = _work_dtype(v.dtype)
+    a = v.to(work)
+    b = ref.to(work) if isinstance(ref, torch.Tensor) else ref
+    return a < b if reduce == "min" else a > b
+
+
+def _carry_args(arg3, improved3, nonempty2, length):
+    """A2 arg state: improving elements keep their position; other elements
+    of nonempty segments take the last improving position of their feature in
+    flattened (batch, segment) order (0 before any); empty segments take
+    `length`."""
+    b, s, f = arg3.shape
+    flat = arg3.reshape(b * s, f)
+    imp = improved3.reshape(b * s, f)
+    pos = torch.arange(b * s, device=arg3.device).view(-1, 1).expand(b * s, f)
+    last = torch.where(imp, pos, torch.full_like(pos, -1)).cummax(0).values
+    carried = torch.where(last >= 0, flat.gather(0, last.clamp_min(0)), torch.zeros_like(flat))
+    ne = nonempty2.reshape(b * s, 1)
+    res = torch.where(ne, torch.where(imp, flat, carried), torch.full_like(flat, length))
+    return res.reshape(b, s, f)
+
+
+def _segment_counts(ptr2d, before, segs):
+    counts = ptr2d[:, 1:] - ptr2d[:, :-1]
+    return counts.expand(before, segs) if counts.size(0) != before else counts
+
+
 # ------------------------------------------------------------------ segment_csr
-def _segment_csr(src, indptr, out, reduce, return_arg):
+def _segment_csr(src, indptr, out, reduce, return_arg, semantics="arch35"):
     _lib.require_gpu(src, indptr, what="segment_csr")
     if indptr.dtype != torch.int64:
         raise RuntimeError(f"indptr must be int64, got {indptr.dtype}")
@@ -123,31 +189,65 @@ def _segment_csr(src, indptr, out, reduce, return_arg):
     src3 = src.contiguous().reshape(before, length, after)
     direct = out is not None and out.is_contiguous()
     out3 = out.view(before, segs, after) if direct else None
+    if semantics == "a2":
+        res3, arg3 = _segment_csr_a2(src3, ptr2d, segs, reduce, return_arg)
+        result = _finish(res3, out, shape)
+        return result, (None if arg3 is None else arg3.reshape(shape))
     res3, arg3 = _native.segment_reduce(src3, ptr2d, segs, _CODE[reduce], _lib.SEM_SEGMENT_CSR, out3,
                                         False, return_arg and reduce in ("min", "max"))
     result = _finish(res3, out, shape)
     return result, (None if arg3 is None else arg3.reshape(shape))
 
 
-def segment_sum_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    return _segment_csr(src, indptr, out, "sum", False)[0]
+def _segment_csr_a2(src3, ptr2d, segs, reduce, return_arg):
+    """A2 segment_csr values / args (reference test/segment_csr/arch22/golden.py:68-153)."""
+    before, length, _ = src3.shape
+    extremum = reduce in ("min", "max")
+    res3, arg3 = _native.segment_reduce(src3, ptr2d, segs, _CODE[reduce], _lib.SEM_SEGMENT_CSR, None, False,
+                                        extremum)
+    counts = _segment_counts(ptr2d, before, segs)
+    if reduce == "mean" and src3.dtype in (torch.float16, torch.bfloat16):
+        # the sum is narrowed to the source dtype, then divided by the count
+        # (itself converted to that dtype)
+        total, _ = _native.segment_reduce(src3, ptr2d, segs, _lib.R_SUM, _lib.SEM_SEGMENT_CSR)
+        div = counts.clamp_min(1).to(torch.float32).to(src3.dtype).unsqueeze(-1)
+        return total / div, None
+    if not extremum:
+        return res3, None
+    nonempty = (counts > 0).unsqueeze(-1)
+    improved = _strictly_better(res3, _identity(src3.dtype, reduce), reduce) & nonempty
+    ident = torch.tensor(_identity(src3.dtype, reduce), dtype=_work_dtype(src3.dtype)).to(src3.dtype)
+    values = torch.where(improved, res3, torch.where(nonempty, ident.to(src3.device), torch.zeros_like(res3)))
+    args = _carry_args(arg3, improved, counts > 0, length) if return_arg else None
+    return values, args
 
 
-def segment_add_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    return _segment_csr(src, indptr, out, "add", False)[0]
+def segment_sum_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                    semantics: str = "arch35") -> torch.Tensor:
+    _check_semantics(semantics)
+    return _segment_csr(src, indptr, out, "sum", False, semantics)[0]
 
 
-def segment_mean_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    return _segment_csr(src, indptr, out, "mean", False)[0]
+def segment_add_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                    semantics: str = "arch35") -> torch.Tensor:
+    _check_semantics(semantics)
+    return _segment_csr(src, indptr, out, "add", False, semantics)[0]
 
 
-def segment_min_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None
-                    ) -> Tuple[torch.Tensor, torch.Tensor]:
-    return _segment_csr(src, indptr, out, "min", True)
+def segment_mean_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                     semantics: str = "arch35") -> torch.Tensor:
+    _check_semantics(semantics)
+    return _segment_csr(src, indptr, out, "mean", False, semantics)[0]
 
 
-def segment_max_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None
-                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+def segment_min_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                    semantics: str = "arch35") -> Tuple[torch.Tensor, torch.Tensor]:
+    _check_semantics(semantics)
+    return _segment_csr(src, indptr, out, "min", True, semantics)
+
+
+def segment_max_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None, *,
+                    semantics: str = "arch35") -> Tuple[torch.Tensor, torch.Tensor]:
     """Values and first indices of the segment maxima.
 
     An int32 indptr selects the legacy value-only entry (segment_max_csr_legacy),
@@ -155,14 +255,17 @@ def segment_max_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch
     """
     if isinstance(indptr, torch.Tensor) and indptr.dtype == torch.int32:
         return segment_max_csr_legacy(src, indptr, out)
-    return _segment_csr(src, indptr, out, "max", True)
+    _check_semantics(semantics)
+    return _segment_csr(src, indptr, out, "max", True, semantics)
 
 
 def segment_csr(src: torch.Tensor, indptr: torch.Tensor, out: Optional[torch.Tensor] = None,
-                reduce: str = "sum") -> torch.Tensor:
-    """Reduce CSR segments along ``indptr.dim() - 1``; values only."""
+                reduce: str = "sum", *, semantics: str = "arch35") -> torch.Tensor:
+    """Reduce CSR segments along ``indptr.dim() - 1``; values only.
+    semantics="a2" selects the reference's Atlas A2 rules (see above)."""
     _check_reduce(reduce)
-    return _segment_csr(src, indptr, out, reduce, False)[0]
+    _check_semantics(semantics)
+    return _segment_csr(src, indptr, out, reduce, False, semantics)[0]
 
 
 def segment_reduce(src: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None,
@@ -204,7 +307,7 @@ def _coo_index_facts(index: torch.Tensor):
     return _COO_FACTS.get(index, compute)
 
 
-def _segment_coo(src, index, out, dim_size, reduce, return_arg):
+def _segment_coo(src, index, out, dim_size, reduce, return_arg, semantics="arch35"):
     _lib.require_gpu(src, index, what="segment_coo")
     if index.dtype != torch.int64:
         raise ValueError("indices must be an int64 tensor with valid rank")
@@ -245,6 +348,11 @@ def _segment_coo(src, index, out, dim_size, reduce, return_arg):
         return res, torch.full(shape, length, dtype=torch.int64, device=src.device)
     ptr2d = _native.sorted_index_ptr(index, segs, idx2d)
     src3 = src.contiguous().reshape(before, length, after)
+    if semantics == "a2":
+        seeds = None if out is None else out.contiguous().reshape(before, segs, after)
+        res3, arg3 = _segment_coo_a2(src3, ptr2d, idx2d, segs, reduce, return_arg, seeds)
+        result = _finish(res3, out, shape)
+        return result, (None if arg3 is None else arg3.reshape(shape))
     has_out = out is not None
     direct = has_out and out.is_contiguous()
     if has_out:
@@ -257,34 +365,87 @@ def _segment_coo(src, index, out, dim_size, reduce, return_arg):
     return result, (None if arg3 is None else arg3.reshape(shape))
 
 
-def segment_sum_coo(src, index, out=None, dim_size=None) -> torch.Tensor:
-    """Sum segments of a sorted index (a supplied out is overwritten, Ascend 950 rule)."""
-    return _segment_coo(src, index, out, dim_size, "sum", False)[0]
+def _segment_coo_a2(src3, ptr2d, idx2d, segs, reduce, return_arg, seeds3):
+    """A2 segment_coo values / args (reference test/segment_coo/arch22/golden.py:63-160)."""
+    before, length, after = src3.shape
+    reduce = "sum" if reduce == "add" else reduce
+    extremum = reduce in ("min", "max")
+    counts = _segment_counts(ptr2d, before, segs)
+    nonempty = (counts > 0).unsqueeze(-1)
+    work = _work_dtype(src3.dtype)
+    if seeds3 is not None:
+        # the segment holding a batch's position 0 starts from out[batch, 0]
+        seeds = seeds3.clone()
+        first = idx2d[:, :1].expand(before, 1) if idx2d.size(0) != before else idx2d[:, :1]
+        seeds.scatter_(1, first.unsqueeze(-1).expand(before, 1, after), seeds3[:, :1, :])
+    if extremum:
+        v, arg3 = _native.segment_reduce(src3, ptr2d, segs, _CODE[reduce], _lib.SEM_SEGMENT_CSR, None, False, True)
+        if seeds3 is None:
+            ident = torch.tensor(_identity(src3.dtype, reduce), dtype=work, device=src3.device)
+            improved = _strictly_better(v, ident, reduce) & nonempty
+            values = torch.where(improved, v, torch.zeros_like(v))
+        else:
+            improved = _strictly_better(v, seeds, reduce) & nonempty
+            values = torch.where(improved, v, seeds3.where(~nonempty, seeds))
+        args = _carry_args(arg3, improved, counts > 0, length) if return_arg else None
+        return values, args
+    total, _ = _native.segment_reduce(src3, ptr2d, segs, _lib.R_SUM, _lib.SEM_SEGMENT_CSR)
+    if seeds3 is not None:
+        total = (seeds.to(work) + total.to(work)).to(src3.dtype) if work != src3.dtype else seeds + total
+    if reduce == "mean":
+        div = counts.to(src3.dtype).unsqueeze(-1)
+        zero = div == 0
+        if src3.dtype.is_floating_point:
+            mean = total / torch.where(zero, torch.ones_like(div), div)
+        else:
+            mean = torch.div(total.to(torch.int64), torch.where(zero, torch.ones_like(div), div).to(torch.int64),
+                             rounding_mode="trunc").to(src3.dtype)
+        total = torch.where(zero, torch.zeros_like(mean), mean)
+    if seeds3 is not None:
+        total = torch.where(nonempty, total, seeds3)
+    else:
+        total = torch.where(nonempty, total, torch.zeros_like(total))
+    return total, None
 
 
-def segment_add_coo(src, index, out=None, dim_size=None) -> torch.Tensor:
-    return segment_sum_coo(src, index, out, dim_size)
+def segment_sum_coo(src, index, out=None, dim_size=None, *, semantics: str = "arch35") -> torch.Tensor:
+    """Sum segments of a sorted index (a supplied out is overwritten, Ascend 950
+    rule; with semantics="a2" it seeds the sums)."""
+    _check_semantics(semantics)
+    return _segment_coo(src, index, out, dim_size, "sum", False, semantics)[0]
 
 
-def segment_mean_coo(src, index, out=None, dim_size=None) -> torch.Tensor:
+def segment_add_coo(src, index, out=None, dim_size=None, *, semantics: str = "arch35") -> torch.Tensor:
+    return segment_sum_coo(src, index, out, dim_size, semantics=semantics)
+
+
+def segment_mean_coo(src, index, out=None, dim_size=None, *, semantics: str = "arch35") -> torch.Tensor:
     """Segment means; a supplied out seeds the numerator."""
-    return _segment_coo(src, index, out, dim_size, "mean", False)[0]
+    _check_semantics(semantics)
+    return _segment_coo(src, index, out, dim_size, "mean", False, semantics)[0]
 
 
-def segment_min_coo(src, index, out=None, dim_size=None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Minima and int64 positions; later ties win (Ascend 950 convention)."""
-    return _segment_coo(src, index, out, dim_size, "min", True)
+def segment_min_coo(src, index, out=None, dim_size=None, *, semantics: str = "arch35"
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Minima and int64 positions; later ties win (Ascend 950 convention;
+    semantics="a2": first strict improvement, carried arg state)."""
+    _check_semantics(semantics)
+    return _segment_coo(src, index, out, dim_size, "min", True, semantics)
 
 
-def segment_max_coo(src, index, out=None, dim_size=None) -> Tuple[torch.Tensor, torch.Tensor]:
-    return _segment_coo(src, index, out, dim_size, "max", True)
+def segment_max_coo(src, index, out=None, dim_size=None, *, semantics: str = "arch35"
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+    _check_semantics(semantics)
+    return _segment_coo(src, index, out, dim_size, "max", True, semantics)
 
 
-def segment_coo(src, index, out=None, dim_size=None, reduce: str = "sum") -> torch.Tensor:
+def segment_coo(src, index, out=None, dim_size=None, reduce: str = "sum", *,
+                semantics: str = "arch35") -> torch.Tensor:
     """Reduce along ``index.dim() - 1`` over a sorted int64 index; values only."""
     if reduce not in _CODE:
         raise ValueError("segment_coo supports sum/add/mean/min/max, not " + str(reduce))
-    return _segment_coo(src, index, out, dim_size, reduce, False)[0]
+    _check_semantics(semantics)
+    return _segment_coo(src, index, out, dim_size, reduce, False, semantics)[0]
 
 
 # ------------------------------------------------------------------ segment_logsumexp
