@@ -640,8 +640,93 @@ void engine_kernel(Params p) {
       if (val_mode == 1) vl_next[t] = ev ? E::load1(val, el) : 0.f;
     }
   };
+  // Long runs (contiguous mode, fast variants, no weights): windows lying
+  // wholly inside the current row -- the bulk of a hub row -- are folded
+  // with no per-step row-end or chunk-end test.  Lane positions and the fold
+  // order per lane are those of the step schedule, so sums and extrema are
+  // the same bits; loads step through src at a uniform stride, FU steps in
+  // flight.  Extrema take 3 VALU per element with the later-tie rule (the
+  // "nothing taken" NaN start becomes -+inf, which every rule treats alike
+  // while the arg is unset); log-sum-exp takes the batch maximum first and
+  // rescales once per batch, one exponential per element.
+  auto long_run = [&](auto minc, int64_t w0, int64_t nwin) {
+    constexpr bool MIN = decltype(minc)::value;
+    constexpr int NSW = kWave / S;           // steps per window
+    constexpr int FU = NSW < 8 ? NSW : 8;    // steps per batch
+    const int64_t stride = (int64_t)S * K;   // elements between steps
+    const S_t* q = srcb + (w0 + sub) * K + k0;
+    int32_t off = (int32_t)(w0 - lo) + sub;  // this lane's position in the chunk
+    if constexpr (RK == RK_MINMAX && VAR == V_LATER) {
+#pragma unroll
+      for (int i = 0; i < NE; ++i)
+        if (best[i] != best[i]) best[i] = MIN ? (MT)__builtin_inff() : (MT)-__builtin_inff();
+    }
+    const int64_t nb = nwin * (NSW / FU);
+    for (int64_t bi = 0; bi < nb; ++bi) {
+      uint4 xr[FU];
+#pragma unroll
+      for (int u = 0; u < FU; ++u) xr[u] = load16(q + u * stride);
+      q += FU * stride;
+      float x[FU][NE];
+#pragma unroll
+      for (int u = 0; u < FU; ++u) E::unpack(xr[u], x[u]);
+      if constexpr (RK == RK_SUM) {
+#pragma unroll
+        for (int u = 0; u < FU; ++u)
+#pragma unroll
+          for (int i = 0; i < NE; ++i) acc[i] = __builtin_fmaf(x[u][i], 1.f, acc[i]);
+      } else if constexpr (RK == RK_MINMAX) {
+#pragma unroll
+        for (int u = 0; u < FU; ++u) {
+          const int32_t pos = off + u * S;
+#pragma unroll
+          for (int i = 0; i < NE; ++i) {
+            const MT pv = (MT)x[u][i];
+            bool take;
+            if constexpr (VAR == V_LATER) take = MIN ? pv <= best[i] : pv >= best[i];
+            else take = !(MIN ? pv >= best[i] : pv <= best[i]) && pv == pv;
+            best[i] = take ? pv : best[i];
+            barg[i] = take ? pos : barg[i];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+          float mx = x[0][i];
+#pragma unroll
+          for (int u = 1; u < FU; ++u) mx = fmaxf(mx, x[u][i]);
+          const float m = (float)best[i];
+          const float nm = fmaxf(m, mx);
+          const float cn = clampf_max(nm);
+          float t = 0.f;
+#pragma unroll
+          for (int u = 0; u < FU; ++u) t += fast_exp(x[u][i] - cn);
+          acc[i] = __builtin_fmaf(acc[i], fast_exp(clampf_max(m) - cn), t);
+          best[i] = nm;
+        }
+      }
+      off += FU * S;
+    }
+  };
+
   stage(lo);
   for (int64_t wbase = lo; wbase < hi; wbase += WPOS) {
+    if constexpr (!GATHER && FAST && VL && WSTEPS == 1 && !IS_INT) {
+      if (val_mode == 0 && r < M) {
+        const int64_t stop = std::min<int64_t>(std::min<int64_t>(re, hi), p.n);
+        const int64_t nwin = (stop - wbase) / WPOS;
+        if (nwin > 0) {
+          if constexpr (RK == RK_MINMAX) {
+            if (is_min) long_run(std::true_type{}, wbase, nwin);
+            else long_run(std::false_type{}, wbase, nwin);
+          } else {
+            long_run(std::false_type{}, wbase, nwin);
+          }
+          wbase += nwin * WPOS;
+          if (wbase >= hi) break;
+        }
+      }
+    }
     // One-step windows copy the staged col / value out and restage at once;
     // multi-step windows read the staged arrays in phase 1 and restage after
     // the gathers are issued (no second copy of the arrays).
@@ -823,6 +908,36 @@ void engine_kernel(Params p) {
 // lanes of its features.  Merges of min/max partials compare (value,
 // position), so the tie rules hold whatever the fold order.
 // INT: int32 sum records (int8 SpMM), finished by finish_int.
+// Long rows: a row whose records span more than kLongSpan chunks has the
+// tail records of its interior chunks (c1, c2) pre-folded in runs that end at
+// multiples of kPiece -- one run per aligned group of kPiece chunks -- into
+// each run's first record, so the fix-up folds about span / kPiece records
+// instead of span (a hub row of config 5 spans ~2000 chunks).
+constexpr int64_t kLongSpan = 64;
+constexpr int64_t kPiece = 32;
+
+struct RowRecords {
+  int64_t c1, c2, first, count;  // first: the first run start past c1 + 1
+  bool lng;
+  // chunk of record t (1 <= t <= count); record count is the head in c2
+  __device__ __forceinline__ int64_t chunk(int64_t t) const {
+    if (!lng) return c1 + t;
+    if (t >= count) return c2;
+    return t == 1 ? c1 + 1 : first + (t - 2) * kPiece;
+  }
+};
+
+__device__ __forceinline__ RowRecords row_records(int64_t c1, int64_t c2) {
+  RowRecords rr;
+  rr.c1 = c1;
+  rr.c2 = c2;
+  rr.lng = c2 - c1 > kLongSpan;
+  rr.first = (c1 + 1) / kPiece * kPiece + kPiece;
+  const int64_t mids = rr.lng && rr.first <= c2 - 1 ? (c2 - 1 - rr.first) / kPiece + 1 : 0;
+  rr.count = rr.lng ? mids + 2 : c2 - c1;
+  return rr;
+}
+
 template <typename MT>
 __device__ __forceinline__ void mm_merge(MT& best, int64_t& barg, MT ob, int64_t oa, bool is_min, bool later,
                                          bool nanprop) {
@@ -843,6 +958,126 @@ __device__ __forceinline__ void mm_merge(MT& best, int64_t& barg, MT ob, int64_t
   if (take) {
     best = ob;
     barg = oa;
+  }
+}
+
+// Pre-fold of long rows (see kLongSpan): one wave per aligned group of
+// kPiece chunks.  Lane l looks at chunk ca + l: it is interior to a long row
+// when the row of its first position started in an earlier chunk c1, ends in
+// a later chunk c2, and c2 - c1 > kLongSpan (the fix-up's test, from the
+// same pointers).  A run starts at max(ca, c1 + 1) and ends at
+// min(ca + kPiece - 1, c2 - 1); its tail records are folded in chunk order
+// (lane groups over records, then a butterfly) into its first record.
+template <typename IDX, int RK, bool F32MM, bool INT = false>
+__global__ __launch_bounds__(kBlock) void prefold_kernel(Params p) {
+  using MT = std::conditional_t<F32MM, double, float>;
+  using AT = std::conditional_t<INT, int32_t, float>;
+  const int lane = lane_id();
+  const int64_t ca = ((int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * kPiece;
+  const int64_t b = blockIdx.z;
+  const int64_t pb = p.ptr_bstride ? b : 0;
+  const IDX* __restrict__ ptr = static_cast<const IDX*>(p.ptr) + pb * p.ptr_bstride;
+  const int64_t base = ptr[0];
+  const int64_t end = std::max<int64_t>(std::min<int64_t>((int64_t)ptr[p.m] - base, p.nnz_bound), 0);
+  const int64_t nce = std::max<int64_t>(1, (end + p.chunk - 1) / p.chunk);
+  if (ca >= nce) return;
+  const int64_t c = ca + lane;
+  bool start = false;
+  int64_t c2 = 0;
+  if (lane < kPiece && c >= 1 && c < nce) {
+    const int64_t r = std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c], 0), p.m - 1);
+    const int64_t rs = ptr[r], re = ptr[r + 1];
+    const int64_t c1 = (rs - base) / p.chunk;
+    c2 = std::min<int64_t>((re - 1 - base) / p.chunk, nce - 1);
+    start = c > c1 && c < c2 && c2 - c1 > kLongSpan && (c == ca || c == c1 + 1);
+  }
+  uint64_t starts = __ballot(start);
+  if (!starts) return;
+  const int64_t K = p.k;
+  const bool is_min = p.reduce == OGN_REDUCE_MIN;
+  const bool is_prod = p.reduce == OGN_REDUCE_PROD;
+  const bool later = p.mm_mode == MM_LATER;
+  const bool nanprop = p.mm_mode == MM_NANPROP;
+  int kw = 1;
+  while (kw < K && kw < kWave) kw <<= 1;
+  const int ng = kWave / kw;
+  const int g = lane / kw;
+  while (starts) {
+    const int sl = __builtin_ctzll(starts);
+    starts &= starts - 1;
+    const int64_t cs = ca + sl;
+    const int64_t ce = std::min<int64_t>(ca + kPiece - 1, (int64_t)readlane64(c2, sl) - 1);
+    if (ce <= cs) continue;
+    for (int64_t k = lane % kw; k < K; k += kw) {
+      const int64_t base_rec = (b * p.nchunks) * K + k;
+      AT a = is_prod ? (AT)1 : (AT)0;
+      MT best = RK == RK_LSE ? (MT)-__builtin_inff() : (MT)0;
+      int64_t barg = kNone;
+      constexpr int B = 8;
+      for (int64_t c0 = cs + g; c0 <= ce; c0 += (int64_t)B * ng) {
+        AT va[B];
+        float vb[B];
+        double vd[B];
+        int64_t vg[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+          const int64_t cc = c0 + (int64_t)j * ng;
+          const bool ok = cc <= ce;
+          const int64_t ri = base_rec + std::min<int64_t>(cc, ce) * K;
+          if constexpr (RK == RK_MINMAX) {
+            vd[j] = ok ? static_cast<const double*>(p.rec_tail)[ri] : 0.0;
+            vg[j] = ok ? p.arg_tail[ri] : kNone;
+          } else if constexpr (RK == RK_LSE) {
+            const float2 t = ok ? static_cast<const float2*>(p.rec_tail)[ri] : make_float2(-__builtin_inff(), 0.f);
+            va[j] = t.x;
+            vb[j] = t.y;
+          } else {
+            va[j] = ok ? static_cast<const AT*>(p.rec_tail)[ri] : (is_prod ? (AT)1 : (AT)0);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+          if constexpr (RK == RK_MINMAX) {
+            mm_merge<MT>(best, barg, (MT)vd[j], vg[j], is_min, later, nanprop);
+          } else if constexpr (RK == RK_LSE) {
+            float m = (float)best;
+            float sa = (float)a;
+            lse_merge(m, sa, (float)va[j], vb[j]);
+            best = m;
+            a = (AT)sa;
+          } else {
+            a = is_prod ? a * va[j] : a + va[j];
+          }
+        }
+      }
+      for (int d = kw; d < kWave; d <<= 1) {
+        if constexpr (RK == RK_MINMAX) {
+          const MT ob = (MT)__shfl_xor((double)best, d);
+          const int64_t oa = __shfl_xor(barg, d);
+          mm_merge<MT>(best, barg, ob, oa, is_min, later, nanprop);
+        } else if constexpr (RK == RK_LSE) {
+          const float om = __shfl_xor((float)best, d), os = __shfl_xor((float)a, d);
+          float m = (float)best;
+          float sa = (float)a;
+          lse_merge(m, sa, om, os);
+          best = m;
+          a = (AT)sa;
+        } else {
+          const AT o = __shfl_xor(a, d);
+          a = is_prod ? a * o : a + o;
+        }
+      }
+      if (g != 0) continue;
+      const int64_t wi = base_rec + cs * K;
+      if constexpr (RK == RK_MINMAX) {
+        static_cast<double*>(p.rec_tail)[wi] = (double)best;
+        p.arg_tail[wi] = barg;
+      } else if constexpr (RK == RK_LSE) {
+        static_cast<float2*>(p.rec_tail)[wi] = make_float2((float)best, (float)a);
+      } else {
+        static_cast<AT*>(p.rec_tail)[wi] = a;
+      }
+    }
   }
 }
 
@@ -867,6 +1102,12 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
   if (fx.x < 0 || fx.x >= p.m) return;
   const int64_t r = fx.x, rs = fx.y, re = fx.z;
   const int64_t c2 = std::min<int64_t>((re - 1 - base) / p.chunk, nce - 1);
+  // Records after the start one, numbered t = 1 .. T: chunks c + 1 .. c2,
+  // or for a long row (prefold_kernel has folded each run of its interior
+  // chunks into the run's first record) c + 1, the run starts at multiples
+  // of kPiece, then c2.
+  const RowRecords rr = row_records(c, c2);
+  const int64_t T = rr.count;
   const int64_t K = p.k;
   const bool is_min = p.reduce == OGN_REDUCE_MIN;
   const bool is_prod = p.reduce == OGN_REDUCE_PROD;
@@ -904,19 +1145,19 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
           a[f] = static_cast<const AT*>(p.rec_tail)[base_rec[f] + c * K];
         }
       }
-      for (int64_t c0 = c + 1; c0 <= c2; c0 += kBatch) {
+      for (int64_t t0 = 1; t0 <= T; t0 += kBatch) {
         AT va[NF][kBatch];
         float vb[NF][kBatch];
         double vd[NF][kBatch];
         int64_t vg[NF][kBatch];
   #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
-          const int64_t cc = c0 + j;
-          const bool ok = cc <= c2;
+          const bool ok = t0 + j <= T;
+          const int64_t cc = rr.chunk(std::min<int64_t>(t0 + j, T));
           const bool head = cc >= c2;
   #pragma unroll
           for (int f = 0; f < NF; ++f) {
-            const int64_t ri = base_rec[f] + std::min<int64_t>(cc, c2) * K;
+            const int64_t ri = base_rec[f] + cc * K;
             if constexpr (RK == RK_MINMAX) {
               vd[f][j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
               vg[f][j] = ok ? (head ? p.arg_head : p.arg_tail)[ri] : kNone;
@@ -999,7 +1240,7 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
         a = static_cast<const AT*>(p.rec_tail)[base_rec + c * K];
       }
     }
-    // fold records c0, c0 + ng, ... (B loads in flight per lane; full: only
+    // fold records t = c0, c0 + ng, ... (B loads in flight per lane; full: only
     // whole batches; returns where it stopped)
     auto fold = [&](auto bc, int64_t from, int64_t to, bool full) -> int64_t {
       constexpr int B = decltype(bc)::value;
@@ -1011,9 +1252,10 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
         int64_t vg[B];
 #pragma unroll
         for (int j = 0; j < B; ++j) {
-          const int64_t cc = c0 + (int64_t)j * ng;
-          const bool ok = cc <= to;
-          const int64_t ri = base_rec + std::min<int64_t>(cc, c2) * K;
+          const int64_t t = c0 + (int64_t)j * ng;
+          const bool ok = t <= to;
+          const int64_t cc = rr.chunk(std::min<int64_t>(t, T));
+          const int64_t ri = base_rec + cc * K;
           const bool head = cc >= c2;
           if constexpr (RK == RK_MINMAX) {
             vd[j] = ok ? static_cast<const double*>(head ? p.rec_head : p.rec_tail)[ri] : 0.0;
@@ -1044,7 +1286,7 @@ __global__ __launch_bounds__(kBlock) void fixup_kernel(Params p) {
       }
       return c0;
     };
-    fold(std::integral_constant<int, 8>{}, c + 1 + g, c2, false);
+    fold(std::integral_constant<int, 8>{}, 1 + g, T, false);
     // merge the lane groups (partners kw, 2kw, ... lanes apart)
     for (int d = kw; d < kWave; d <<= 1) {
       if constexpr (RK == RK_MINMAX) {

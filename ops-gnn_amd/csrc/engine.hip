@@ -124,6 +124,32 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
         break;
     }
   }
+  if (pl.nchunks > kLongSpan + 1) {
+    // rows spanning more than kLongSpan chunks: fold their interior records
+    // in runs of kPiece first
+    TimedLaunch t((n + "_prefold").c_str(), s);
+    const int64_t groups = (pl.nchunks + kPiece - 1) / kPiece;
+    const dim3 pg((unsigned)((groups + kWavesPerBlock - 1) / kWavesPerBlock), 1, (unsigned)batch);
+    const bool f32mm = rk == RK_MINMAX && in_dtype == OGN_F32;
+#define OGN_PRE(IDX)                                                                          \
+  switch (rk) {                                                                               \
+    case RK_MINMAX:                                                                           \
+      if (f32mm) hipLaunchKernelGGL((prefold_kernel<IDX, RK_MINMAX, true>), pg, dim3(kBlock), 0, s, p); \
+      else hipLaunchKernelGGL((prefold_kernel<IDX, RK_MINMAX, false>), pg, dim3(kBlock), 0, s, p);     \
+      break;                                                                                  \
+    case RK_LSE: hipLaunchKernelGGL((prefold_kernel<IDX, RK_LSE, false>), pg, dim3(kBlock), 0, s, p); break; \
+    default: hipLaunchKernelGGL((prefold_kernel<IDX, RK_SUM, false>), pg, dim3(kBlock), 0, s, p); break;     \
+  }
+    if (in_dtype == OGN_I8 && rk == RK_SUM) {
+      if (i64) hipLaunchKernelGGL((prefold_kernel<int64_t, RK_SUM, false, true>), pg, dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL((prefold_kernel<int32_t, RK_SUM, false, true>), pg, dim3(kBlock), 0, s, p);
+    } else if (i64) {
+      OGN_PRE(int64_t)
+    } else {
+      OGN_PRE(int32_t)
+    }
+#undef OGN_PRE
+  }
   if (pl.nchunks > 1) {
     TimedLaunch t((n + "_fixup").c_str(), s);
     const dim3 fg((unsigned)((pl.nchunks + kWavesPerBlock - 1) / kWavesPerBlock), 1, (unsigned)batch);
