@@ -241,7 +241,25 @@ int ogn_ptr2ind(const void* ptr, int index_dtype, int64_t rows, int64_t numel, i
  * csrc/npu/segment_coo/op_host/segment_coo.cpp:1127-1175).
  */
 enum { OGN_SEM_SEGMENT_CSR = 0, OGN_SEM_SEGMENT_COO = 1, OGN_SEM_SCATTER = 2, OGN_SEM_DGL = 3 };
-enum { OGN_SEG_HAS_OUT = 1 };
+/* flags:
+ *  OGN_SEG_HAS_OUT -- out holds seeds (see semantics above).
+ *  OGN_SEG_SHORT_SEGMENTS -- the caller knows that no segment holds more
+ *    than 4096 rows; the pass that pre-folds the partial results of segments
+ *    spanning many wavefront chunks is then not launched.
+ *  OGN_SEG_KEEP_LAYOUT -- the caller keeps `workspace` for later calls with
+ *    the same indptr (same address, same contents) on the same stream; the
+ *    library records which pointer array and chunk plan the workspace's
+ *    chunk layout (row of every chunk's first position, rows crossing chunk
+ *    ends) was computed for.
+ *  OGN_SEG_REUSE_LAYOUT -- `workspace` was last used with KEEP or REUSE for
+ *    this indptr, whose contents have not changed since: the chunk-row pass
+ *    is skipped when the recorded pointer address and plan match this call
+ *    (otherwise the layout is recomputed and recorded).  The rest of the
+ *    workspace is rewritten by every call, so calls sharing one workspace
+ *    must not overlap.
+ * No counterpart in the reference (its host tiling is recomputed per call);
+ * they serve callers that run one graph many times. */
+enum { OGN_SEG_HAS_OUT = 1, OGN_SEG_SHORT_SEGMENTS = 2, OGN_SEG_KEEP_LAYOUT = 4, OGN_SEG_REUSE_LAYOUT = 8 };
 size_t ogn_segment_reduce_workspace_size(int64_t batch, int64_t length, int64_t segments, int64_t k,
                                          int64_t ptr_batches, int dtype, int reduce);
 int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* src, int dtype,

@@ -1341,8 +1341,15 @@ Workspace workspace_layout(const Plan& pl, int64_t k, int64_t batch, int64_t ptr
 
 // Run the engine: chunk-row pass, main pass, fix-up pass.  `name` labels the
 // launches for the opt-in timer (<name>_main etc.).
+// Layout options of run(): no row longer than 64 * the smallest chunk (4096
+// positions: the long-row pre-fold is skipped), and keeping / reusing the
+// chunk layout (chunk_row, fix) of a workspace across calls with one
+// pointer array.
+enum { LAYOUT_SHORT_ROWS = 1, LAYOUT_KEEP = 2, LAYOUT_REUSE = 4 };
+constexpr int64_t kShortRowsMax = 4096;
+
 int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, int rk, int64_t batch,
-        void* workspace, size_t workspace_bytes, hipStream_t s, const char* name);
+        void* workspace, size_t workspace_bytes, hipStream_t s, const char* name, int layout = 0);
 
 // Per-dtype / per-mode instantiations (engine_<mode>_<dt>.hip).
 #define OGN_ENGINE_DECL(NAME) \

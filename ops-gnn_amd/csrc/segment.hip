@@ -624,8 +624,11 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
       p.limit = dtype == OGN_F32 ? 3.4028234663852886e38f : (dtype == OGN_F16 ? 65504.f : 3.3895313892515355e38f);
       break;
   }
+  const int layout = ((flags & OGN_SEG_SHORT_SEGMENTS) ? LAYOUT_SHORT_ROWS : 0) |
+                     ((flags & OGN_SEG_KEEP_LAYOUT) ? LAYOUT_KEEP : 0) |
+                     ((flags & OGN_SEG_REUSE_LAYOUT) ? LAYOUT_REUSE : 0);
   return run(pl, p, dtype, OGN_I64, false, rk, batch, workspace, workspace_bytes,
-             static_cast<hipStream_t>(stream), "segment");
+             static_cast<hipStream_t>(stream), "segment", layout);
 }
 
 int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,

@@ -94,6 +94,10 @@ MSG_MUL, MSG_ADD, MSG_SUB, MSG_DIV = range(4)
 SPMM_TORCH_SPARSE, SPMM_DGL = range(2)
 SDDMM_OPS = {"dot": 0, "add": 1, "sub": 2, "mul": 3, "div": 4, "copy_lhs": 5, "copy_rhs": 6}
 SEG_HAS_OUT = 1
+SEG_SHORT_SEGMENTS = 2  # no segment holds more than SHORT_SEGMENT_MAX rows
+SEG_KEEP_LAYOUT = 4
+SEG_REUSE_LAYOUT = 8
+SHORT_SEGMENT_MAX = 4096
 
 for _name, (_res, _args) in SIGNATURES.items():
     _fn = getattr(_so, _name)

@@ -111,13 +111,41 @@ SEGMENT_EXACT_DTYPES = (torch.int8, torch.uint8, torch.int32, torch.int64)
 SCATTER_DTYPES = SEGMENT_DTYPES + (torch.float64, torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8)
 
 
+# Engine workspaces kept per pointer tensor version: a graph reduced many
+# times reuses its chunk layout (ogn.h OGN_SEG_REUSE_LAYOUT).  Bounded in
+# entries and in bytes per workspace.
+_LAYOUT_WS = None
+_LAYOUT_WS_MAX_BYTES = 256 << 20
+
+
+def _layout_workspace(key: torch.Tensor, sub: tuple, nbytes: int, device):
+    """(workspace, flags): a kept workspace for (key's version, sub) -- REUSE
+    when it already holds the layout, else a new one with KEEP."""
+    global _LAYOUT_WS
+    if _LAYOUT_WS is None:
+        _LAYOUT_WS = _VersionCache(limit=8)
+    per_key = _LAYOUT_WS.get(key, dict)
+    ws = per_key.get(sub)
+    if ws is not None:
+        return ws, _lib.SEG_REUSE_LAYOUT
+    ws = _lib.workspace(nbytes, device)
+    per_key.clear()  # one shape / stream per pointer version is the common case
+    per_key[sub] = ws
+    return ws, _lib.SEG_KEEP_LAYOUT
+
+
 def segment_reduce(src3: torch.Tensor, ptr2d: torch.Tensor, segments: int, reduce: int, semantics: int,
-                   out3: Optional[torch.Tensor] = None, has_out: bool = False, need_arg: bool = False
+                   out3: Optional[torch.Tensor] = None, has_out: bool = False, need_arg: bool = False,
+                   key: Optional[torch.Tensor] = None, max_len: Optional[int] = None
                    ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Contiguous-segment reduction (include/ogn.h ogn_segment_reduce).
 
     src3 [B, L, F] contiguous; ptr2d int64 [1 | B, S+1] contiguous; out3
     [B, S, F] contiguous (holding seeds when has_out).  Returns (out3, arg3).
+    key: a tensor whose version certifies ptr2d's contents (the caller's
+    pointer or index tensor, or ptr2d itself when it is a cached tensor);
+    the engine workspace is then kept with its chunk layout.  max_len: the
+    longest segment, when the caller knows it.
     """
     b, length, f = src3.shape
     if out3 is None:
@@ -128,10 +156,18 @@ def segment_reduce(src3: torch.Tensor, ptr2d: torch.Tensor, segments: int, reduc
     pb = ptr2d.shape[0]
     code = _lib.TORCH_TO_OGN[src3.dtype]
     ws_bytes = lib.ogn_segment_reduce_workspace_size(b, length, segments, f, pb, code, reduce)
-    ws = _lib.workspace(ws_bytes, src3.device)
+    flags = _lib.SEG_HAS_OUT if has_out else 0
+    if max_len is not None and max_len <= _lib.SHORT_SEGMENT_MAX:
+        flags |= _lib.SEG_SHORT_SEGMENTS
+    stream = stream_of(src3)
+    if key is not None and 0 < ws_bytes <= _LAYOUT_WS_MAX_BYTES and src3.dtype not in SEGMENT_EXACT_DTYPES:
+        sub = (ptr2d.data_ptr(), tuple(ptr2d.shape), b, length, segments, f, code, reduce, stream.value, ws_bytes)
+        ws, lf = _layout_workspace(key, sub, ws_bytes, src3.device)
+        flags |= lf
+    else:
+        ws = _lib.workspace(ws_bytes, src3.device)
     rc = lib.ogn_segment_reduce(dptr(ptr2d), pb, dptr(src3), code, b, length, segments, f, dptr(out3), dptr(arg),
-                                reduce, semantics, _lib.SEG_HAS_OUT if has_out else 0, dptr(ws), ws_bytes,
-                                stream_of(src3))
+                                reduce, semantics, flags, dptr(ws), ws_bytes, stream)
     check(rc, "segment reduction")
     return out3, arg
 

@@ -131,7 +131,8 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
         use_segments = _native.index_facts(line, key=index)[0]
     if use_segments:
         ptr = _native.sorted_index_ptr(index, size, line.reshape(1, -1))
-        res3, arg3 = _native.segment_reduce(src3, ptr, size, code, _lib.SEM_SCATTER, out3, has_out, is_minmax)
+        res3, arg3 = _native.segment_reduce(src3, ptr, size, code, _lib.SEM_SCATTER, out3, has_out, is_minmax,
+                                            key=ptr)
     else:
         if compact:
             idx, strides = line.contiguous(), (0, 1, 0)

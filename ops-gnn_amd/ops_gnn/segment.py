@@ -43,16 +43,19 @@ def _split(shape, dim):
 
 
 def _pointer_facts(ptr2d: torch.Tensor):
-    """(non-decreasing and >= 0, max) of a pointer tensor: one small
-    device-to-host read, cached per tensor version.  Pass the caller's own
-    tensor (not a fresh view of it) so that the cache can hit."""
+    """(non-decreasing and >= 0, max, longest segment) of a pointer tensor:
+    one small device-to-host read, cached per tensor version.  Pass the
+    caller's own tensor (not a fresh view of it) so that the cache can hit."""
     def compute():
         p = ptr2d
         bad = (p < 0).any()
+        longest = torch.zeros((), dtype=p.dtype, device=p.device)
         if p.size(-1) > 1:
-            bad = bad | (p[..., 1:] < p[..., :-1]).any()
-        flags = torch.stack((bad.to(torch.int64), p.max())).tolist()
-        return flags[0] == 0, flags[1]
+            steps = p[..., 1:] - p[..., :-1]
+            bad = bad | (steps < 0).any()
+            longest = steps.max()
+        flags = torch.stack((bad.to(torch.int64), p.max().to(torch.int64), longest.to(torch.int64))).tolist()
+        return flags[0] == 0, flags[1], flags[2]
     return _PTR_FACTS.get(ptr2d, compute)
 
 
@@ -179,7 +182,7 @@ def _segment_csr(src, indptr, out, reduce, return_arg, semantics="arch35"):
     else:
         ptr2d = indptr.expand(*src.shape[:dim], segs + 1).reshape(before, segs + 1).contiguous()
     # broadcasting repeats pointer rows, so the facts of indptr are those of ptr2d
-    ok, top = _pointer_facts(indptr)
+    ok, top, longest = _pointer_facts(indptr)
     if not ok:
         raise RuntimeError("indptr must be nondecreasing and non-negative")
     if top > length:
@@ -194,7 +197,8 @@ def _segment_csr(src, indptr, out, reduce, return_arg, semantics="arch35"):
         result = _finish(res3, out, shape)
         return result, (None if arg3 is None else arg3.reshape(shape))
     res3, arg3 = _native.segment_reduce(src3, ptr2d, segs, _CODE[reduce], _lib.SEM_SEGMENT_CSR, out3,
-                                        False, return_arg and reduce in ("min", "max"))
+                                        False, return_arg and reduce in ("min", "max"), key=indptr,
+                                        max_len=longest)
     result = _finish(res3, out, shape)
     return result, (None if arg3 is None else arg3.reshape(shape))
 
@@ -360,7 +364,7 @@ def _segment_coo(src, index, out, dim_size, reduce, return_arg, semantics="arch3
     else:
         out3 = None
     res3, arg3 = _native.segment_reduce(src3, ptr2d, segs, _CODE[reduce], _lib.SEM_SEGMENT_COO, out3, has_out,
-                                        return_arg and reduce in ("min", "max"))
+                                        return_arg and reduce in ("min", "max"), key=ptr2d)
     result = _finish(res3, out, shape)
     return result, (None if arg3 is None else arg3.reshape(shape))
 
@@ -478,8 +482,11 @@ def segment_logsumexp(src: torch.Tensor, indptr: torch.Tensor, out: Optional[tor
     def compute():
         # the reference reads these back on every call (segment_logsumexp.py:75-84);
         # here once per indptr version
+        steps = ptr[1:] - ptr[:-1]
+        longest = steps.max() if steps.numel() else torch.zeros((), dtype=torch.int64, device=ptr.device)
         return tuple(int(v) for v in torch.stack(((ptr < 0).any().to(torch.int64),
-                                                  (ptr[1:] < ptr[:-1]).any().to(torch.int64), ptr[-1])).tolist())
+                                                  (steps < 0).any().to(torch.int64), ptr[-1],
+                                                  longest)).tolist())
     flags = _LSE_FACTS.get(indptr, compute)
     if int(flags[0]):
         raise ValueError("indptr must be non-negative")
@@ -508,7 +515,7 @@ def segment_logsumexp(src: torch.Tensor, indptr: torch.Tensor, out: Optional[tor
         length = src.size(0)
         after = math.prod(src.shape[1:])
         res3, _ = _native.segment_reduce(src.contiguous().reshape(1, length, after), ptr.reshape(1, -1), segs,
-                                         _lib.R_LSE, _lib.SEM_SEGMENT_CSR)
+                                         _lib.R_LSE, _lib.SEM_SEGMENT_CSR, key=indptr, max_len=int(flags[3]))
         result = res3.reshape(shape)
     if out is not None:
         out.copy_(result)

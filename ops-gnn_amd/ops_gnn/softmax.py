@@ -130,7 +130,7 @@ class _GroupedLogSumExp(torch.autograd.Function):
         src3 = src.contiguous().reshape(shape3)
         if is_sorted:
             ptr = _native.sorted_index_ptr(index, groups)
-            res3, _ = _native.segment_reduce(src3, ptr, groups, _lib.R_LSE, _lib.SEM_SEGMENT_CSR)
+            res3, _ = _native.segment_reduce(src3, ptr, groups, _lib.R_LSE, _lib.SEM_SEGMENT_CSR, key=ptr)
         else:
             m, s = _stats(src3, index, groups, False)
             res3 = _native.group_lse_from_stats(m, s, src.dtype)
