@@ -1348,6 +1348,23 @@ Workspace workspace_layout(const Plan& pl, int64_t k, int64_t batch, int64_t ptr
 enum { LAYOUT_SHORT_ROWS = 1, LAYOUT_KEEP = 2, LAYOUT_REUSE = 4 };
 constexpr int64_t kShortRowsMax = 4096;
 
+// Fingerprint of a layout kept in a caller workspace: the workspace, the
+// pointer array and the plan values it was computed for (v[0] names the
+// layout kind: 0 engine chunk layout, 1 grouped-softmax long-row list).
+struct KeptKey {
+  const void* ws;
+  const void* ptr;
+  int64_t v[8];
+  bool same(const KeptKey& o) const {
+    if (ws != o.ws || ptr != o.ptr) return false;
+    for (int i = 0; i < 8; ++i)
+      if (v[i] != o.v[i]) return false;
+    return true;
+  }
+};
+bool kept_layout_match(const KeptKey& k);
+void kept_layout_store(const KeptKey& k);
+
 int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, int rk, int64_t batch,
         void* workspace, size_t workspace_bytes, hipStream_t s, const char* name, int layout = 0);
 

@@ -78,33 +78,24 @@ Workspace workspace_layout(const Plan& pl, int64_t k, int64_t batch, int64_t ptr
   return w;
 }
 
-// Chunk layouts kept in caller workspaces (LAYOUT_KEEP / LAYOUT_REUSE): which
-// pointer array and plan each workspace's chunk_row / fix sections were
-// computed for.  A small list (most recent last), bounded.
+// Layouts kept in caller workspaces (LAYOUT_KEEP / LAYOUT_REUSE, and the
+// long-row list of the grouped softmax): which pointer array and plan each
+// workspace's layout was computed for.  A small list (most recent last),
+// bounded.
 namespace {
-struct KeptLayout {
-  const void* ws;
-  const void* ptr;
-  int64_t ptr_bstride, ptr_batches, m, nnz_bound, chunk, nchunks;
-  int index_dtype;
-  bool same(const KeptLayout& o) const {
-    return ws == o.ws && ptr == o.ptr && ptr_bstride == o.ptr_bstride && ptr_batches == o.ptr_batches &&
-           m == o.m && nnz_bound == o.nnz_bound && chunk == o.chunk && nchunks == o.nchunks &&
-           index_dtype == o.index_dtype;
-  }
-};
 std::mutex g_kept_mu;
-std::vector<KeptLayout> g_kept;
+std::vector<KeptKey> g_kept;
 constexpr size_t kKeptMax = 64;
+}  // namespace
 
-bool layout_is_kept(const KeptLayout& k) {
+bool kept_layout_match(const KeptKey& k) {
   std::lock_guard<std::mutex> lock(g_kept_mu);
-  for (const KeptLayout& e : g_kept)
+  for (const KeptKey& e : g_kept)
     if (e.same(k)) return true;
   return false;
 }
 
-void layout_keep(const KeptLayout& k) {
+void kept_layout_store(const KeptKey& k) {
   std::lock_guard<std::mutex> lock(g_kept_mu);
   for (size_t i = 0; i < g_kept.size(); ++i) {
     if (g_kept[i].ws == k.ws) {
@@ -115,7 +106,6 @@ void layout_keep(const KeptLayout& k) {
   if (g_kept.size() >= kKeptMax) g_kept.erase(g_kept.begin());
   g_kept.push_back(k);
 }
-}  // namespace
 
 int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, int rk, int64_t batch,
         void* workspace, size_t workspace_bytes, hipStream_t s, const char* name, int layout) {
@@ -140,14 +130,14 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
   // contiguous mode, fast variants: chunks of short rows take short_chunk
   p.short_rows = !gather && in_dtype != OGN_I8 && variant_of(rk, false, p) != V_GENERIC &&
                  !std::getenv("OGN_ENGINE_NO_SHORT");
-  const KeptLayout kl{workspace, p.ptr, p.ptr_bstride, ptr_batches, p.m, p.nnz_bound, pl.chunk, pl.nchunks,
-                      index_dtype};
-  if (!(layout & LAYOUT_REUSE) || !layout_is_kept(kl)) {
+  const KeptKey kl{workspace, p.ptr, {0, p.ptr_bstride, ptr_batches, p.m, p.nnz_bound, pl.chunk, pl.nchunks,
+                                       index_dtype}};
+  if (!(layout & LAYOUT_REUSE) || !kept_layout_match(kl)) {
     TimedLaunch t((n + "_chunk_rows").c_str(), s);
     const dim3 g((unsigned)((pl.nchunks + 255) / 256), (unsigned)ptr_batches);
     if (i64) hipLaunchKernelGGL(chunk_rows_kernel<int64_t>, g, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(chunk_rows_kernel<int32_t>, g, dim3(256), 0, s, p);
-    if (layout & (LAYOUT_KEEP | LAYOUT_REUSE)) layout_keep(kl);
+    if (layout & (LAYOUT_KEEP | LAYOUT_REUSE)) kept_layout_store(kl);
   }
   const dim3 grid((unsigned)((pl.nchunks + kWavesPerBlock - 1) / kWavesPerBlock), (unsigned)pl.tiles,
                   (unsigned)batch);

@@ -224,6 +224,39 @@ def test_grouped_softmax_register_row_sizes(ogn, oracle, dtype, mode):
     _softmax_check(ogn, oracle, src, torch.from_numpy(idx), 1, deg.size, mode, SOFT_TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax"])
+@pytest.mark.parametrize("before", [1, 2])
+def test_grouped_softmax_repeated_calls(ogn, oracle, dtype, mode, before):
+    # Repeated calls with one index tensor (its group pointers are cached):
+    # rows straddling the register tiers of the row and long-row kernels, a
+    # poisoned long row; every call is checked, and again after the index
+    # changes in place (new version, pointers rebuilt).
+    v = 8 if dtype != torch.float32 else 4
+    sizes = [1, 64 * v, 256 * v, 256 * v + 1, 512 * v + 3, 1024 * v, 1024 * v + 1, 3000 * v, 0, 7, 300,
+             256 * v + 1, 5, 2048 * v + 9]
+    rng = np.random.default_rng(55)
+    deg = np.array(sizes, dtype=np.int64)
+    idx = np.repeat(np.arange(deg.size), deg)
+    x = (rng.standard_normal((before, idx.size)) * 5).astype(np.float32)
+    starts = np.concatenate([[0], np.cumsum(deg)])
+    x[0, starts[7] + 100] = INF  # a long row poisoned
+    src = torch.from_numpy(x).to(dtype)
+    index = torch.from_numpy(idx).cuda()
+    fn = ogn.scatter_softmax if mode == "softmax" else ogn.scatter_log_softmax
+    for step in range(5):
+        if step == 3:
+            # move a boundary in place: the list is rebuilt for the new version
+            j = int(starts[2])
+            index[j: j + 40] = 1
+            idx[j: j + 40] = 1
+        got = fn(src.cuda(), index, 1, deg.size).float().cpu().numpy()
+        gold = cast_like(oracle.group_softmax(src, torch.from_numpy(idx), 1, deg.size, mode), dtype)
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(gold))
+        np.testing.assert_allclose(got, gold, rtol=SOFT_TOL[dtype], atol=SOFT_TOL[dtype], equal_nan=True,
+                                   err_msg=f"call {step}")
+
+
 @pytest.mark.parametrize("sorted_index", [True, False])
 def test_grouped_softmax_special_values(ogn, oracle, sorted_index):
     src = torch.tensor([INF, 1.0, -INF, 2.0, NAN, 0.0, -INF, -INF])
