@@ -231,12 +231,43 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Dot of two 16-byte feature packets, accumulated in fp32: fp16 and bf16
+// pairs go through v_dot2c_f32_f16 / v_dot2c_f32_bf16 (products of 16-bit
+// values are exact in fp32), four instructions per packet; fp32 packets take
+// four FMAs.
+template <int DT>
+__device__ __forceinline__ float packet_dot(const uint4& a, const uint4& b, float d) {
+  if constexpr (DT == OGN_F16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.x), __builtin_bit_cast(h2, b.x), d, false);
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.y), __builtin_bit_cast(h2, b.y), d, false);
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.z), __builtin_bit_cast(h2, b.z), d, false);
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.w), __builtin_bit_cast(h2, b.w), d, false);
+  } else if constexpr (DT == OGN_BF16) {
+    typedef short s2 __attribute__((ext_vector_type(2)));
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.x), __builtin_bit_cast(s2, b.x), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.y), __builtin_bit_cast(s2, b.y), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.z), __builtin_bit_cast(s2, b.z), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.w), __builtin_bit_cast(s2, b.w), d, false);
+  } else {
+    d = __builtin_fmaf(__uint_as_float(a.x), __uint_as_float(b.x), d);
+    d = __builtin_fmaf(__uint_as_float(a.y), __uint_as_float(b.y), d);
+    d = __builtin_fmaf(__uint_as_float(a.z), __uint_as_float(b.z), d);
+    d = __builtin_fmaf(__uint_as_float(a.w), __uint_as_float(b.w), d);
+  }
+  return d;
+}
+
 // dot(lhs[row(e)], rhs[col(e)]) -- the GAT score and the SpMM edge-weight
 // gradient.  Specialises the generic kernel for that case: the lhs row is
 // held in registers and reloaded only when a sub-group's row changes, rhs
 // rows are gathered U at a time with 32-bit byte offsets from a uniform
-// base, the sub-group reduction uses DPP, and column indices of the next
-// window are loaded one window ahead.
+// base, packets are dotted with the dot2 instructions, the sub-group
+// reduction uses DPP, and column indices of the next window are loaded one
+// window ahead.  A block of U steps lying inside the current row (most of
+// them: rows are long) skips the per-step row walk.  The 64 results of a
+// window are gathered one per lane -- lane s * G + j keeps step j of
+// sub-group s -- and written with one store.
 template <int DT, typename IDX, int G>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4)))
 void sddmm_dot_kernel(SddmmParams p) {
@@ -244,7 +275,8 @@ void sddmm_dot_kernel(SddmmParams p) {
   using S_t = typename E::S;
   constexpr int NE = E::VEC;
   constexpr int S = kWave / G;
-  constexpr int U = 8;
+  constexpr int NSTEPS = kWave / S;  // steps per 64-edge window (= G)
+  constexpr int U = NSTEPS < 8 ? NSTEPS : 8;
   const int lane = lane_id();
   const int sub = lane / G;
   const int gl = lane % G;
@@ -275,6 +307,12 @@ void sddmm_dot_kernel(SddmmParams p) {
 
   int64_t held = -1;
   uint4 keep = make_uint4(0u, 0u, 0u, 0u);
+  auto hold = [&](int64_t row) {
+    if (row != held) {  // rare: a new row for this sub-group
+      held = row;
+      keep = held < p.lhs_rows ? load16(lhs + (uint64_t)held * row_bytes + k_off) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
   int32_t cl_next = 0;
   auto stage = [&](int64_t w) {
     const int64_t el = w + lane;
@@ -286,13 +324,31 @@ void sddmm_dot_kernel(SddmmParams p) {
     if (wbase + kWave < hi) stage(wbase + kWave);
     const int nw = (int)std::min<int64_t>(kWave, hi - wbase);
     const int nsteps = (nw + S - 1) / S;
+    float mine = 0.f;  // this lane's result: step gl of sub-group sub
     for (int j0 = 0; j0 < nsteps; j0 += U) {
-      int64_t row[U];
       uint32_t co[U];
 #pragma unroll
+      for (int u = 0; u < U; ++u) co[u] = (uint32_t)shfl32(cl, ((j0 + u) * S + sub) & (kWave - 1)) * row_bytes + k_off;
+      uint4 xr[U];
+#pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int idx = (j0 + u) * S + sub;
-        co[u] = (uint32_t)shfl32(cl, idx & (kWave - 1)) * row_bytes + k_off;
+        const bool ok = (j0 + u) < nsteps && (j0 + u) * S + sub < nw;
+        xr[u] = ok ? load16(rhs + co[u]) : make_uint4(0u, 0u, 0u, 0u);
+      }
+      const int64_t block_last = wbase + std::min<int64_t>((int64_t)(j0 + U) * S, nw) - 1;
+      if (block_last < re) {
+        // every edge of the block is in row r
+        hold(r);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float d = group_sum<G>(packet_dot<DT>(keep, xr[u], 0.f));
+          if (gl == j0 + u) mine = d;
+        }
+        continue;
+      }
+      int64_t row[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
         row[u] = 0;
         if (j0 + u >= nsteps) continue;
         const int64_t e_first = wbase + (int64_t)(j0 + u) * S;
@@ -309,31 +365,16 @@ void sddmm_dot_kernel(SddmmParams p) {
           re = rowend(r);
         }
       }
-      uint4 xr[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int idx = (j0 + u) * S + sub;
-        const bool ok = (j0 + u) < nsteps && idx < nw;
-        xr[u] = ok ? load16(rhs + co[u]) : make_uint4(0u, 0u, 0u, 0u);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int idx = (j0 + u) * S + sub;
-        const bool ok = (j0 + u) < nsteps && idx < nw;
-        if (ok && row[u] != held) {  // rare: a new row for this sub-group
-          held = row[u];
-          keep = held < p.lhs_rows ? load16(lhs + (uint64_t)held * row_bytes + k_off) : make_uint4(0u, 0u, 0u, 0u);
-        }
-        float xl[NE], xv[NE];
-        E::unpack(keep, xl);
-        E::unpack(xr[u], xv);
-        float d = 0.f;
-#pragma unroll
-        for (int i = 0; i < NE; ++i) d = __builtin_fmaf(xl[i], xv[i], d);
-        d = group_sum<G>(d);
-        if (gl == 0 && ok) store_floats<1>(p.out, p.dt, wbase + idx, &d);
+        const bool ok = (j0 + u) < nsteps && (j0 + u) * S + sub < nw;
+        if (ok) hold(row[u]);
+        const float d = group_sum<G>(packet_dot<DT>(keep, xr[u], 0.f));
+        if (gl == j0 + u) mine = d;
       }
     }
+    const int idx = gl * S + sub;  // window edge of this lane's result
+    if (idx < nw) store_floats<1>(p.out, p.dt, wbase + idx, &mine);
   }
 }
 
