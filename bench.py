@@ -62,41 +62,64 @@ def copy_calibration():
     del src, dst
 
 
-def measure_copy_gbs(nbytes=1 << 30, reps=5):
-    """Practical HBM ceiling: a device-to-device copy of `nbytes` (read +
-    write counted), timed with HIP events on the current stream."""
+def _event_ms(fn, reps=5):
+    """Mean ms of fn() over `reps` calls after one warm call, HIP events on the current stream."""
     import torch
 
-    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
-    dst = torch.empty_like(src)
-    dst.copy_(src)
+    fn()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(reps):
-        dst.copy_(src)
+        fn()
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / reps
+    return start.elapsed_time(end) / reps
+
+
+def _stream_gbs(copy, nbytes=1 << 30):
+    """Practical HBM ceilings from the library's streaming kernel
+    (ogn_calibrate_stream, 16-byte packets, 8 in flight per thread): a copy
+    of `nbytes` (read + write counted) or a read of `nbytes`."""
+    import torch
+
+    from ops_gnn import _lib
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src) if copy else None
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+
+    def run():
+        _lib.check(_lib.lib.ogn_calibrate_stream(_lib.dptr(src), _lib.dptr(dst), nbytes, _lib.dptr(sink),
+                                                 _lib.stream_of(src)), "calibrate_stream")
+    ms = _event_ms(run)
     del src, dst
-    return round(2 * nbytes / (ms * 1e-3) / 1e9, 1)
+    return round((2 if copy else 1) * nbytes / (ms * 1e-3) / 1e9, 1)
 
 
-def measure_read_gbs(nbytes=1 << 30, reps=5):
-    """Practical read-only HBM ceiling: torch's sum over `nbytes` of fp32
-    (the SpMM gather is read-dominated), timed with HIP events."""
+def measure_copy_gbs():
+    return _stream_gbs(True)
+
+
+def measure_read_gbs():
+    return _stream_gbs(False)
+
+
+def gather_floor_ms(table, index):
+    """Time to read exactly the rows `index` selects from `table` [rows, k]
+    and nothing else (ogn_calibrate_gather): the floor of any kernel that
+    gathers them."""
     import torch
 
-    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
-    src.sum()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        src.sum()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / reps
-    del src
-    return round(nbytes / (ms * 1e-3) / 1e9, 1)
+    from ops_gnn import _lib
+
+    rows = table.shape[0]
+    row_bytes = table[0].numel() * table.element_size()
+    sink = torch.zeros(1, dtype=torch.int32, device=table.device)
+
+    def run():
+        _lib.check(_lib.lib.ogn_calibrate_gather(_lib.dptr(table), rows, row_bytes, _lib.dptr(index), index.numel(),
+                                                 _lib.dptr(sink), _lib.stream_of(table)), "calibrate_gather")
+    return _event_ms(run)
 
 
 def torch_sparse_mm_baseline(ptr, col, val, mat, rows):
@@ -239,7 +262,9 @@ def main():
             copy_calibration()
         copy_gbs = measure_copy_gbs()
         read_gbs = measure_read_gbs()
-        log(f"bench: device copy {copy_gbs} GB/s, device read (sum) {read_gbs} GB/s (practical ceilings)")
+        gather_ms = gather_floor_ms(d_mat, d_col)
+        log(f"bench: streaming copy {copy_gbs} GB/s, streaming read {read_gbs} GB/s, gathering the "
+            f"{nnz} rows alone {gather_ms:.3f} ms (practical ceilings)")
 
         torch_ms = None
         if args.torch_compare and args.reduce == "sum":
@@ -309,7 +334,11 @@ def main():
             "kernel_ms": round(kernel_ms, 4),
             "copy_ceiling": copy_gbs,
             "read_ceiling": read_gbs,
-            "frac_of_read_ceiling": round(achieved / read_gbs, 4),
+            # the same rows gathered by ogn_calibrate_gather, nothing else
+            # read or written: no SpMM over this graph can take less
+            "gather_floor_ms": round(gather_ms, 4),
+            "gather_floor_GB/s": round(nnz * k * esz / (gather_ms * 1e-3) / 1e9, 1),
+            "kernel_over_gather_floor": round(kernel_ms / gather_ms, 4),
         },
         "cpu_baseline": cpu,
     }
@@ -490,8 +519,12 @@ def bench_gat(args):
                 f"compulsory {comp[name] / ms / 1e6:.1f} GB/s")
         ms = _timed(layer, args.steps, args.warmup)
         km = _kernel_ms(layer, args.steps, ["sddmm_main", "spmm_main", "segment_softmax", "group_apply", "segment_stats_main"])
+        gfloor = gather_floor_ms(kk, col)
+        log(f"bench gat: gathering the {e} K rows alone {gfloor:.3f} ms")
     tot_eff = sum(eff.values())
     ops["layer"] = {"ms": round(ms, 4), "kernels_ms": {k2: round(v2, 4) for k2, v2 in km.items()}}
+    ops["gather_floor"] = {"ms": round(gfloor, 4), "GB/s": round(2 * e * f / (gfloor * 1e-3) / 1e9, 1),
+                           "note": "the e K (or V) rows of 128 B that sddmm (SpMM) gathers, read alone"}
     log(f"bench gat layer: {ms:.4f} ms; kernels {km}")
     cpu = None
     if not args.no_cpu_baseline:

@@ -387,6 +387,21 @@ int ogn_gather_csr(const int64_t* indptr, int64_t ptr_batches, const void* src, 
 int ogn_gather_coo(const int64_t* index, const void* src, int64_t batch, int64_t src_rows, int64_t entries,
                    int64_t row_bytes, void* out, void* stream);
 
+/* ------------------------------------------------------------------ measurement
+ * Practical memory ceilings, reported by bench.py beside the 8 TB/s HBM
+ * peak.  No counterpart in the reference; they serve measurement only.
+ * ogn_calibrate_gather: reads table rows index[0 .. n) (row_bytes each, 16 *
+ *   a power of two up to 1024; table 16-byte aligned, below 4 GiB; indices
+ *   clamped into [0, rows)) exactly as a gathering kernel would, and nothing
+ *   else: the time floor of any kernel gathering those rows.
+ * ogn_calibrate_stream: streaming copy of `bytes` (a multiple of 16) from
+ *   src to dst, or a streaming read of src when dst is NULL.
+ * sink: one 4-byte device word, written only under a condition that never
+ * holds (it keeps the loads live). */
+int ogn_calibrate_gather(const void* table, int64_t rows, int64_t row_bytes, const int64_t* index, int64_t n,
+                         void* sink, void* stream);
+int ogn_calibrate_stream(const void* src, void* dst, int64_t bytes, void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -85,6 +85,8 @@ SIGNATURES = {
     "ogn_gather_coo": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "ogn_group_softmax_backward": (_int, [_vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _int, _vp,
                                           _vp, _sz, _vp]),
+    "ogn_calibrate_gather": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "ogn_calibrate_stream": (_int, [_vp, _vp, _i64, _vp, _vp]),
 }
 
 # reduce / semantics codes (include/ogn.h)
