@@ -320,8 +320,10 @@ constexpr int engine_waves() {
 // chunk's rows are dealt to the S sub-groups in turn, each sub-group folds
 // its row's positions (four loads in flight) on its own -- no cross-lane
 // combine -- and finishes the row, or leaves the same head / tail record as
-// the step schedule for a row that crosses the chunk's edge.
-template <int DT, int G, bool VL, int RK, int VAR>
+// the step schedule for a row that crosses the chunk's edge.  The extremum
+// direction is a template parameter, and argument positions are int32
+// offsets from the chunk start.
+template <int DT, int G, bool VL, int RK, int VAR, bool MIN>
 __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t lo, int64_t hi, int64_t r0,
                                             int64_t r_end) {
   using E = Elem<DT>;
@@ -338,34 +340,40 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
   const int64_t M = p.m;
   const int64_t k0 = (int64_t)blockIdx.y * (G * NE) + gl * NE;
   const bool kok = VL || k0 < K;
+  const int64_t kc = kok ? k0 : 0;  // a feature in range for the loads
   const int64_t* __restrict__ ptr = static_cast<const int64_t*>(p.ptr) + pb * p.ptr_bstride;
   const S_t* __restrict__ srcb = static_cast<const S_t*>(p.src) + b * p.src_bstride;
-  const bool is_min = p.reduce == OGN_REDUCE_MIN;
   // rows r0 .. r_end - 1 end inside the chunk; r_end (< m) may start inside it
   const int64_t r_last = std::min<int64_t>(r_end, M - 1);
   for (int64_t r = r0 + sub; r <= r_last; r += S) {
     const int64_t rs = ptr[r], re = ptr[r + 1];
     if (r == r_end && rs >= hi) break;  // starts in the next chunk
-    const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(re, hi);
+    const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(std::min<int64_t>(re, hi), p.n);
     float acc[NE], best[NE];
-    int64_t barg[NE];
+    int32_t barg[NE];
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
       acc[i] = 0.f;
-      best[i] = RK == RK_LSE ? -__builtin_inff() : __builtin_nanf("");  // NaN: nothing taken yet
-      barg[i] = kNone;
+      // later tie: -+inf start, "nothing taken" while the arg is unset;
+      // first tie: NaN start (no ordered compare with it holds)
+      best[i] = RK == RK_LSE ? -__builtin_inff()
+                             : (VAR == V_LATER ? (MIN ? __builtin_inff() : -__builtin_inff()) : __builtin_nanf(""));
+      barg[i] = kNone32;
     }
     for (int64_t e0 = a; e0 < z; e0 += kU) {
       float x[kU][NE];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        const bool ok = e0 + u < z && kok;
+        // conditional: most of these rows hold 1-2 positions, and loading
+        // all four packets regardless was measured 15 % slower
+        const bool ok = e0 + u < z;
         if constexpr (VL) {
-          E::unpack(ok ? load16(srcb + (e0 + u) * K + k0) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+          E::unpack(ok ? load16(srcb + (e0 + u) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
         } else {
-          x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + k0) : 0.f;
+          x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + kc) : 0.f;
         }
       }
+      const int32_t off = (int32_t)(e0 - lo);
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         if (e0 + u >= z) break;
@@ -373,11 +381,11 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
         for (int i = 0; i < NE; ++i) {
           const float pv = x[u][i];
           if constexpr (RK == RK_MINMAX) {
-            const bool blocked = VAR == V_LATER ? (is_min ? pv > best[i] : pv < best[i])
-                                                : (is_min ? pv >= best[i] : pv <= best[i]);
-            const bool take = !(pv != pv) && !blocked;
+            bool take;
+            if constexpr (VAR == V_LATER) take = MIN ? pv <= best[i] : pv >= best[i];
+            else take = !(MIN ? pv >= best[i] : pv <= best[i]) && pv == pv;
             best[i] = take ? pv : best[i];
-            barg[i] = take ? e0 + u : barg[i];
+            barg[i] = take ? off + u : barg[i];
           } else if constexpr (RK == RK_LSE) {
             lse_add(best[i], acc[i], pv);
           } else {
@@ -395,7 +403,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
       for (int i = 0; i < NE; ++i) {
         if constexpr (RK == RK_MINMAX) {
           static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)best[i];
-          (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i];
+          (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i] == kNone32 ? kNone : lo + barg[i];
         } else if constexpr (RK == RK_LSE) {
           static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2(best[i], acc[i]);
         } else {
@@ -407,7 +415,9 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
       float v[NE];
       int64_t ag[NE];
 #pragma unroll
-      for (int i = 0; i < NE; ++i) finish_elem<RK, float>(p, b, r, k0 + i, rs, re, acc[i], best[i], barg[i], &v[i], &ag[i]);
+      for (int i = 0; i < NE; ++i)
+        finish_elem<RK, float>(p, b, r, k0 + i, rs, re, acc[i], best[i], barg[i] == kNone32 ? kNone : lo + barg[i],
+                               &v[i], &ag[i]);
       store_floats<NE, true>(p.out, p.out_dt, off, v);
       if constexpr (RK == RK_MINMAX) {
         if (p.arg) {
@@ -470,7 +480,8 @@ void engine_kernel(Params p) {
     if (p.short_rows) {
       const int64_t r_end = chunk_row_end(p, pb, c, nce);
       if (chunk_is_short(r, r_end, lo, hi, S)) {
-        short_chunk<DT, G, VL, RK, VAR>(p, c, lo, hi, r, r_end);
+        if (RK == RK_MINMAX && is_min) short_chunk<DT, G, VL, RK, VAR, true>(p, c, lo, hi, r, r_end);
+        else short_chunk<DT, G, VL, RK, VAR, false>(p, c, lo, hi, r, r_end);
         return;
       }
     }
@@ -500,14 +511,36 @@ void engine_kernel(Params p) {
   // Extremum positions are held as int32 offsets from the chunk start (a
   // chunk is at most 8192 positions); kNone32 marks "nothing taken".
   int32_t barg[NE];
+  // Fast variants keep extrema in "max space": a min reduction folds -x with
+  // the max rules (flipv negates under a uniform mask, one VALU, no
+  // per-element choice between two compares), and values are flipped back
+  // where they leave the wave (records, finishing).  Negation is exact, so
+  // values, ties and signed zeros come back unchanged.
+  constexpr bool MAXSPACE = FAST && RK == RK_MINMAX;
+  const bool flip_mm = MAXSPACE && is_min;
+  auto flipv = [&](MT v) -> MT {
+    if constexpr (!MAXSPACE) {
+      return v;
+    } else if constexpr (std::is_same<MT, double>::value) {
+      const uint64_t u = (uint64_t)__double_as_longlong(v) ^ (flip_mm ? 0x8000000000000000ull : 0ull);
+      return __longlong_as_double((long long)u);
+    } else {
+      return __uint_as_float(__float_as_uint(v) ^ (flip_mm ? 0x80000000u : 0u));
+    }
+  };
+  const bool mm_min = MAXSPACE ? false : is_min;  // direction of the compares below
   auto reset = [&]() {
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
       acc[i] = is_prod ? (AT)1 : (AT)0;
       // min/max start from NaN, "nothing taken yet": every ordered compare
       // with it is false, so the first non-NaN message is taken without a
-      // separate test (barg stays kNone32 until then)
-      best[i] = RK == RK_LSE ? (MT)-__builtin_inff() : (MT)__builtin_nan("");
+      // separate test (barg stays kNone32 until then).  The later-tie fast
+      // variant starts from -inf instead (max space): taking on >= then
+      // needs one compare, and -inf with no arg is "nothing taken" to every
+      // rule that reads the state.
+      best[i] = RK == RK_LSE ? (MT)-__builtin_inff()
+                             : (VAR == V_LATER ? (MT)-__builtin_inff() : (MT)__builtin_nan(""));
       barg[i] = kNone32;
     }
   };
@@ -531,12 +564,12 @@ void engine_kernel(Params p) {
           take = oa != kNone32 &&
                  (barg[i] == kNone32 ||
                   (their_nan ? (!mine_nan || oa < barg[i])
-                             : (!mine_nan && (better(ob, best[i], is_min) || (ob == best[i] && oa < barg[i])))));
+                             : (!mine_nan && (better(ob, best[i], mm_min) || (ob == best[i] && oa < barg[i])))));
         } else if (later) {
-          take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
+          take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], mm_min) ||
                                    (ob == best[i] && oa > barg[i]));
         } else {
-          take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], is_min) ||
+          take = oa != kNone32 && (barg[i] == kNone32 || better(ob, best[i], mm_min) ||
                                    (ob == best[i] && oa < barg[i]));
         }
         best[i] = take ? ob : best[i];
@@ -575,7 +608,7 @@ void engine_kernel(Params p) {
     for (int i = 0; i < NE; ++i) {
       if (!VL && k0 + i >= K) break;
       if constexpr (RK == RK_MINMAX) {
-        static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)best[i];
+        static_cast<double*>(head ? p.rec_head : p.rec_tail)[rb + i] = (double)flipv(best[i]);
         (head ? p.arg_head : p.arg_tail)[rb + i] = barg[i] == kNone32 ? kNone : lo + barg[i];
       } else if constexpr (RK == RK_LSE) {
         static_cast<float2*>(head ? p.rec_head : p.rec_tail)[rb + i] = make_float2((float)best[i], (float)acc[i]);
@@ -602,7 +635,7 @@ void engine_kernel(Params p) {
       } else {
 #pragma unroll
         for (int i = 0; i < NE; ++i)
-          finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, (float)acc[i], best[i],
+          finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, (float)acc[i], flipv(best[i]),
                               barg[i] == kNone32 ? kNone : lo + barg[i], &v[i], &ag[i]);
         if (VL || k0 + NE <= K) {
           store_floats<NE, true>(p.out, p.out_dt, off, v);
@@ -656,10 +689,14 @@ void engine_kernel(Params p) {
     const int64_t stride = (int64_t)S * K;   // elements between steps
     const S_t* q = srcb + (w0 + sub) * K + k0;
     int32_t off = (int32_t)(w0 - lo) + sub;  // this lane's position in the chunk
-    if constexpr (RK == RK_MINMAX && VAR == V_LATER) {
+    if constexpr (RK == RK_MINMAX) {
+      // the state is kept in max space; fold in the real direction here
 #pragma unroll
-      for (int i = 0; i < NE; ++i)
-        if (best[i] != best[i]) best[i] = MIN ? (MT)__builtin_inff() : (MT)-__builtin_inff();
+      for (int i = 0; i < NE; ++i) {
+        best[i] = flipv(best[i]);
+        if constexpr (VAR == V_LATER)
+          if (best[i] != best[i]) best[i] = MIN ? (MT)__builtin_inff() : (MT)-__builtin_inff();
+      }
     }
     const int64_t nb = nwin * (NSW / FU);
     for (int64_t bi = 0; bi < nb; ++bi) {
@@ -706,6 +743,10 @@ void engine_kernel(Params p) {
         }
       }
       off += FU * S;
+    }
+    if constexpr (RK == RK_MINMAX) {
+#pragma unroll
+      for (int i = 0; i < NE; ++i) best[i] = flipv(best[i]);
     }
   };
 
@@ -841,15 +882,16 @@ void engine_kernel(Params p) {
             for (int i = 0; i < NE; ++i) {
               const float wi = wcur[NW > 1 ? i : 0];
               if constexpr (RK == RK_MINMAX) {
-                const MT pv = apply_op<MT>((MT)x[i], (MT)wi, vop);
                 // selects, not branches: lanes disagree on `take` all the time
+                const MT pv = flipv(apply_op<MT>((MT)x[i], (MT)wi, vop));
                 const bool isnan_pv = pv != pv;
                 bool take;
                 if constexpr (FAST) {
-                  // NaN-ignoring; `blocked` is false against the NaN start
-                  const bool blocked = VAR == V_LATER ? (is_min ? pv > best[i] : pv < best[i])
-                                                      : (is_min ? pv >= best[i] : pv <= best[i]);
-                  take = !isnan_pv && !blocked;
+                  // max space, NaN-ignoring: later tie takes on >= from the
+                  // -inf start; first tie on >, where the NaN start takes
+                  // any number
+                  if constexpr (VAR == V_LATER) take = pv >= best[i];
+                  else take = !(pv <= best[i]) && !isnan_pv;
                 } else {
                   // NaN-propagating: the first NaN is kept (its position is the arg)
                   take = nanprop ? (barg[i] == kNone32 || (isnan_pv && best[i] == best[i]) ||
