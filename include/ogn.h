@@ -301,14 +301,21 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
  * positions, a 256-thread block per longer row: meant for rows of >= ~64
  * positions on average.  src and out 16-byte aligned, and length * element
  * size a multiple of 16 when batch > 1.  Workspace (256-byte aligned, its
- * contents need no initialisation): the long-row list,
- * ogn_segment_group_softmax_workspace_size() bytes.  Fuses the sorted-index
+ * contents need no initialisation): the long-row list and a row plan,
+ * ogn_segment_group_softmax_workspace_size() bytes.  flags: with
+ * OGN_SEG_KEEP_LAYOUT (or REUSE without a kept plan) the call also bins the
+ * rows by length into the workspace (a plan for later calls; this call then
+ * waits for a 64-byte read of the bin counts); with OGN_SEG_REUSE_LAYOUT and a
+ * plan kept for this workspace, indptr address and shape, short rows share
+ * wavefronts (8, 16 or 32 lanes per row) and the rows run largest first.
+ * Calls sharing a kept workspace must not overlap; indptr must be unchanged
+ * since the plan was built.  ABI 3 added `flags`.  Fuses the sorted-index
  * forward phases of scatter_softmax / scatter_log_softmax (reference
  * csrc/npu/scatter_softmax/common/grouped_softmax_shared.h:178-209). */
 size_t ogn_segment_group_softmax_workspace_size(int64_t batch, int64_t length, int64_t segments, int dtype);
 int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
-                              int64_t segments, void* out, int log_softmax, void* workspace, size_t workspace_bytes,
-                              void* stream);
+                              int64_t segments, void* out, int log_softmax, int flags, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ unsorted scatter
  * torch_scatter scatter with an arbitrary int64 index (same rules as

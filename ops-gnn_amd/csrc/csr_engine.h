@@ -1397,6 +1397,7 @@ struct KeptKey {
   const void* ws;
   const void* ptr;
   int64_t v[8];
+  int64_t payload[8];  // host facts kept with the layout (not part of the key)
   bool same(const KeptKey& o) const {
     if (ws != o.ws || ptr != o.ptr) return false;
     for (int i = 0; i < 8; ++i)
@@ -1405,6 +1406,8 @@ struct KeptKey {
   }
 };
 bool kept_layout_match(const KeptKey& k);
+// as kept_layout_match, also copying out the stored payload on a match
+bool kept_layout_find(const KeptKey& k, int64_t* payload);
 void kept_layout_store(const KeptKey& k);
 
 int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, int rk, int64_t batch,

@@ -88,12 +88,19 @@ std::vector<KeptKey> g_kept;
 constexpr size_t kKeptMax = 64;
 }  // namespace
 
-bool kept_layout_match(const KeptKey& k) {
+bool kept_layout_find(const KeptKey& k, int64_t* payload) {
   std::lock_guard<std::mutex> lock(g_kept_mu);
-  for (const KeptKey& e : g_kept)
-    if (e.same(k)) return true;
+  for (const KeptKey& e : g_kept) {
+    if (e.same(k)) {
+      if (payload)
+        for (int i = 0; i < 8; ++i) payload[i] = e.payload[i];
+      return true;
+    }
+  }
   return false;
 }
+
+bool kept_layout_match(const KeptKey& k) { return kept_layout_find(k, nullptr); }
 
 void kept_layout_store(const KeptKey& k) {
   std::lock_guard<std::mutex> lock(g_kept_mu);
@@ -131,7 +138,7 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
   p.short_rows = !gather && in_dtype != OGN_I8 && variant_of(rk, false, p) != V_GENERIC &&
                  !std::getenv("OGN_ENGINE_NO_SHORT");
   const KeptKey kl{workspace, p.ptr, {0, p.ptr_bstride, ptr_batches, p.m, p.nnz_bound, pl.chunk, pl.nchunks,
-                                       index_dtype}};
+                                       index_dtype}, {}};
   if (!(layout & LAYOUT_REUSE) || !kept_layout_match(kl)) {
     TimedLaunch t((n + "_chunk_rows").c_str(), s);
     const dim3 g((unsigned)((pl.nchunks + 255) / 256), (unsigned)ptr_batches);

@@ -142,7 +142,7 @@ int ogn_timing_query(const char* kernel, double* total_ms, int64_t* launches) {
   return OGN_OK;
 }
 const char* ogn_arch(void) { return "gfx950"; }
-int ogn_abi_version(void) { return 2; }
+int ogn_abi_version(void) { return 3; }
 
 int ogn_validate_csr(const void* rowptr, const void* col, int index_dtype, int64_t m,
                      int64_t nnz, int64_t n, int32_t* status, void* stream) {

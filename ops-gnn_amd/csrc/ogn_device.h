@@ -294,6 +294,13 @@ __device__ __forceinline__ double xor_shfl(double v) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
+// This wavefront's index in its block, as a wave-uniform (scalar) value:
+// the compiler does not know that threadIdx.x >> 6 is uniform, and code
+// indexed by it otherwise runs as vector code with serialised scalar loads.
+__device__ __forceinline__ int wave_in_block() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }

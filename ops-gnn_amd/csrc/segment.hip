@@ -136,7 +136,7 @@ template <int DT>
 __global__ __launch_bounds__(256) void row_stats_k1_kernel(const int64_t* __restrict__ ptr, const void* __restrict__ src,
                                                            int64_t length, int64_t segments, float* __restrict__ m_out,
                                                            float* __restrict__ s_out) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave_in_block();
   if (r >= segments) return;
   const int64_t b = blockIdx.y;
   const int64_t rs = std::max<int64_t>(ptr[r], 0);
@@ -324,7 +324,7 @@ __global__ __launch_bounds__(256) void row_softmax_k1_kernel(const int64_t* __re
                                                              int64_t segments, void* __restrict__ out, int log_mode,
                                                              LongRowList list) {
   using E = Elem<DT>;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave_in_block();
   if (r >= segments) return;
   const int64_t b = blockIdx.y;
   const int64_t rs = std::max<int64_t>(ptr[r], 0);
@@ -337,7 +337,9 @@ __global__ __launch_bounds__(256) void row_softmax_k1_kernel(const int64_t* __re
   if (packets <= 2 * kWave) return softmax_row_in_registers<DT, 2>(row, out, obase, rs, re, length, log_mode);
   if (packets <= 3 * kWave) return softmax_row_in_registers<DT, 3>(row, out, obase, rs, re, length, log_mode);
   if (packets <= 4 * kWave) return softmax_row_in_registers<DT, 4>(row, out, obase, rs, re, length, log_mode);
-  if (lane_id() == 0) list.rows[atomicAdd(list.count, 1ull)] = b * segments + r;
+  // a long row: listed for row_softmax_long_kernel (no list: a kept plan
+  // already holds the long rows)
+  if (list.rows && lane_id() == 0) list.rows[atomicAdd(list.count, 1ull)] = b * segments + r;
 }
 
 // Reduction over a 256-thread block: wave_reduce64, then the 4 wave
@@ -426,7 +428,8 @@ template <int DT>
 __global__ __launch_bounds__(256) void row_softmax_long_kernel(const int64_t* __restrict__ ptr,
                                                                const void* __restrict__ src, int64_t length,
                                                                int64_t segments, void* __restrict__ out,
-                                                               int log_mode, LongRowList list) {
+                                                               int log_mode, LongRowList list,
+                                                               const longlong2* __restrict__ bounds) {
   using E = Elem<DT>;
   constexpr int V = E::VEC;
   constexpr int UB = 8;
@@ -435,12 +438,23 @@ __global__ __launch_bounds__(256) void row_softmax_long_kernel(const int64_t* __
   const int t = (int)threadIdx.x;
   const int64_t count = (int64_t)*list.count;
   for (int64_t item = blockIdx.x; item < count; item += gridDim.x) {
-    const int64_t code = list.rows[item];
-    const int64_t b = code / segments, r = code - b * segments;
+    // a row code b * segments + r of the list, or (bounds given: a kept
+    // plan) the row's clamped [start, end) in batch blockIdx.y
+    int64_t b, rs, re;
+    if (bounds) {
+      const longlong2 bd = bounds[item];
+      b = blockIdx.y;
+      rs = bd.x;
+      re = bd.y;
+    } else {
+      const int64_t code = list.rows[item];
+      b = code / segments;
+      const int64_t r = code - b * segments;
+      rs = std::max<int64_t>(ptr[r], 0);
+      re = std::min<int64_t>(ptr[r + 1], length);
+    }
     const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
     const int64_t obase = b * length;
-    const int64_t rs = std::max<int64_t>(ptr[r], 0);
-    const int64_t re = std::min<int64_t>(ptr[r + 1], length);
     const int64_t q0 = rs / V * V;
     const uint32_t n = (uint32_t)(re - rs);
     const int64_t pk = row_packets<DT>(rs, re);
@@ -525,6 +539,270 @@ __global__ __launch_bounds__(256) void row_softmax_long_kernel(const int64_t* __
   }
 }
 
+// ---------------------------------------------------------------- binned rows
+// A kept softmax plan (one per pointer array, built on a KEEP call) lists the
+// rows by class of 16-byte packets per row:
+//   0: <= 8 packets -- 8-lane groups, 8 rows per wavefront
+//   1: <= 16        -- 16-lane groups, 4 rows per wavefront
+//   2: <= 32        -- 32-lane groups, 2 rows per wavefront
+//   3..6: <= 64 / 128 / 192 / 256 -- one wavefront, 1..4 packets per lane
+//   7: longer       -- a 256-thread block per row (row_softmax_long_kernel)
+// Empty rows are in no class.  Rows of one wavefront each leave most lanes
+// idle when they are short (a 64-position fp16 row is 8 packets); packing
+// them lets every lane load a packet.  The binned launch orders classes
+// from the largest rows to the smallest.
+constexpr int kSmClasses = 8;
+constexpr int kSmPacked = 7;  // classes run by the binned kernel
+
+__host__ __device__ constexpr int sm_rows_per_wave(int c) { return c == 0 ? 8 : (c == 1 ? 4 : (c == 2 ? 2 : 1)); }
+
+__device__ __forceinline__ int sm_class(int64_t packets) {
+  if (packets <= 0) return -1;
+  if (packets <= 8) return 0;
+  if (packets <= 16) return 1;
+  if (packets <= 32) return 2;
+  if (packets <= 64) return 3;
+  if (packets <= 128) return 4;
+  if (packets <= 192) return 5;
+  if (packets <= 256) return 6;
+  return 7;
+}
+
+struct SmPlan {
+  int64_t row_off[kSmClasses + 1];  // class c's rows: rows[row_off[c] .. row_off[c + 1])
+  int64_t wave_off[kSmPacked];      // first wavefront of class c in the binned launch
+  int64_t waves[kSmPacked];         // wavefronts of class c
+  int64_t total;                    // wavefronts of the binned launch
+};
+
+// Binning pays when short rows are common: with fewer than 1/8 of the rows
+// in the 8 / 16 / 32-lane classes, rows run one wavefront each in row order
+// (row_softmax_k1_kernel), which measured faster for rows of 33-256 packets
+// (uniform 491-position fp16 rows: 0.093 ms in row order, 0.113 ms binned).
+bool sm_plan_binned(const int64_t* counts) {
+  int64_t shortr = 0, all = 0;
+  for (int c = 0; c < kSmClasses; ++c) {
+    all += counts[c];
+    if (c < 3) shortr += counts[c];
+  }
+  return shortr * 8 >= all;
+}
+
+SmPlan sm_plan_from_counts(const int64_t* counts) {
+  SmPlan pl{};
+  pl.row_off[0] = 0;
+  for (int c = 0; c < kSmClasses; ++c) pl.row_off[c + 1] = pl.row_off[c] + counts[c];
+  int64_t w = 0;
+  for (int c = kSmPacked - 1; c >= 0; --c) {  // largest rows first
+    pl.wave_off[c] = w;
+    pl.waves[c] = (counts[c] + sm_rows_per_wave(c) - 1) / sm_rows_per_wave(c);
+    w += pl.waves[c];
+  }
+  pl.total = w;
+  return pl;
+}
+
+// Workspace of the plan: counts[8], cursor[8] (u64), then the rows'
+// clamped bounds (16 bytes each: one load gives a wavefront its row).
+struct SmPlanSpace {
+  unsigned long long* counts;
+  unsigned long long* cursor;
+  longlong2* rows;  // clamped [start, end) of each listed row
+};
+
+__global__ void sm_zero_kernel(unsigned long long* p, int n) {
+  if ((int)threadIdx.x < n) p[threadIdx.x] = 0ull;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void sm_plan_count_kernel(const int64_t* __restrict__ ptr, int64_t length,
+                                                            int64_t segments, unsigned long long* counts) {
+  __shared__ unsigned int h[kSmClasses];
+  if (threadIdx.x < kSmClasses) h[threadIdx.x] = 0u;
+  __syncthreads();
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < segments) {
+    const int64_t rs = std::max<int64_t>(ptr[r], 0), re = std::min<int64_t>(ptr[r + 1], length);
+    const int c = sm_class(row_packets<DT>(rs, re));
+    if (c >= 0) atomicAdd(&h[c], 1u);
+  }
+  __syncthreads();
+  if (threadIdx.x < kSmClasses && h[threadIdx.x]) atomicAdd(&counts[threadIdx.x], (unsigned long long)h[threadIdx.x]);
+}
+
+__global__ void sm_plan_scan_kernel(const unsigned long long* counts, unsigned long long* cursor) {
+  if (threadIdx.x != 0) return;
+  unsigned long long a = 0;
+  for (int c = 0; c < kSmClasses; ++c) {
+    cursor[c] = a;
+    a += counts[c];
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void sm_plan_scatter_kernel(const int64_t* __restrict__ ptr, int64_t length,
+                                                              int64_t segments, unsigned long long* cursor,
+                                                              longlong2* __restrict__ rows) {
+  __shared__ unsigned int h[kSmClasses];
+  __shared__ unsigned long long base[kSmClasses];
+  if (threadIdx.x < kSmClasses) h[threadIdx.x] = 0u;
+  __syncthreads();
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int c = -1;
+  unsigned int local = 0;
+  int64_t rs = 0, re = 0;
+  if (r < segments) {
+    rs = std::max<int64_t>(ptr[r], 0);
+    re = std::min<int64_t>(ptr[r + 1], length);
+    c = sm_class(row_packets<DT>(rs, re));
+    if (c >= 0) local = atomicAdd(&h[c], 1u);
+  }
+  __syncthreads();
+  if (threadIdx.x < kSmClasses && h[threadIdx.x])
+    base[threadIdx.x] = atomicAdd(&cursor[threadIdx.x], (unsigned long long)h[threadIdx.x]);
+  __syncthreads();
+  if (c >= 0) rows[base[c] + local] = make_longlong2(rs, re);
+}
+
+// Reduction over aligned groups of L lanes (8, 16 or 32): DPP inside each
+// 16-lane row, then one cross-row exchange for 32.  Every lane of a group
+// ends with the same bits.
+template <int L, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  v = op(v, dpp(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  if constexpr (L >= 16) v = op(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+  if constexpr (L >= 32) v = op(v, xor_shfl<16>(v));
+  return v;
+}
+
+// Softmax / log_softmax of up to 64 / L rows of at most L packets, one per
+// L-lane group, one packet per lane; `valid` false: the group has no row.
+template <int DT, int L>
+__device__ __forceinline__ void softmax_rows_grouped(const typename Elem<DT>::S* __restrict__ row,
+                                                     void* __restrict__ out, int64_t obase, int64_t rs, int64_t re,
+                                                     int64_t length, int log_mode) {
+  using E = Elem<DT>;
+  constexpr int V = E::VEC;
+  const int gl = (int)lane_id() % L;
+  const int64_t q0 = rs / V * V;
+  const int64_t q = q0 + (int64_t)gl * V;
+  const uint32_t n = (uint32_t)(re - rs);
+  const uint4 raw = length >= V ? load16(row + packet_address<DT>(q, q0, re, length)) : make_uint4(0u, 0u, 0u, 0u);
+  float x[V];
+  if (q < re && q + V > length) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) x[i] = q + i < length ? E::load1(row, q + i) : 0.f;
+  } else {
+    E::unpack(raw, x);
+  }
+  const int32_t d = (int32_t)(q - rs);
+  float pm = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    x[i] = (uint32_t)(d + i) < n ? x[i] : -__builtin_inff();
+    pm = fmaxf(pm, x[i]);
+  }
+  const float m = group_reduce<L, true>(pm);
+  const float cm = clampf_max(m);
+  float ps = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const float e = fast_exp(x[i] - cm);
+    ps += e;
+    if (!log_mode) x[i] = e;
+  }
+  const float s = group_reduce<L, false>(ps);
+  float inv, ls;
+  softmax_row_constants(m, s, inv, ls);
+  if (q >= re) return;
+  float v[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) v[i] = log_mode ? (x[i] - cm) - ls : x[i] * inv;
+  if (d >= 0 && (uint32_t)(d + V) <= n) {
+    store_floats<V, true>(out, DT, obase + q, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if ((uint32_t)(d + i) < n) store_floats<1>(out, DT, obase + q + i, &v[i]);
+  }
+}
+
+template <int DT, int L>
+__device__ __forceinline__ void binned_groups(const typename Elem<DT>::S* row, void* out, int64_t obase,
+                                              int64_t length, int log_mode, const longlong2* __restrict__ rows,
+                                              int64_t first, int64_t last) {
+  const int64_t i = first + (int64_t)(lane_id() / L);
+  const longlong2 bd = i < last ? rows[i] : make_longlong2(0, 0);
+  softmax_rows_grouped<DT, L>(row, out, obase, bd.x, bd.y, length, log_mode);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void row_softmax_binned_kernel(const void* __restrict__ src, int64_t length,
+                                                                 void* __restrict__ out, int log_mode,
+                                                                 const longlong2* __restrict__ rows, SmPlan plan) {
+  using E = Elem<DT>;
+  const int64_t w = (int64_t)blockIdx.x * 4 + wave_in_block();
+  if (w >= plan.total) return;
+  int c = 0;
+#pragma unroll
+  for (int k = 0; k < kSmPacked; ++k)
+    if (w >= plan.wave_off[k] && w < plan.wave_off[k] + plan.waves[k]) c = k;
+  const int64_t idx = w - plan.wave_off[c];
+  const int64_t b = blockIdx.y;
+  const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
+  const int64_t obase = b * length;
+  const int64_t first = plan.row_off[c] + idx * sm_rows_per_wave(c), last = plan.row_off[c + 1];
+  switch (c) {
+    case 0: return binned_groups<DT, 8>(row, out, obase, length, log_mode, rows, first, last);
+    case 1: return binned_groups<DT, 16>(row, out, obase, length, log_mode, rows, first, last);
+    case 2: return binned_groups<DT, 32>(row, out, obase, length, log_mode, rows, first, last);
+    default: break;
+  }
+  const longlong2 bd = rows[first];
+  const int64_t rs = bd.x, re = bd.y;
+  if (c == 3) return softmax_row_in_registers<DT, 1>(row, out, obase, rs, re, length, log_mode);
+  if (c == 4) return softmax_row_in_registers<DT, 2>(row, out, obase, rs, re, length, log_mode);
+  if (c == 5) return softmax_row_in_registers<DT, 3>(row, out, obase, rs, re, length, log_mode);
+  return softmax_row_in_registers<DT, 4>(row, out, obase, rs, re, length, log_mode);
+}
+
+template <int DT>
+void launch_softmax_plan(hipStream_t st, const int64_t* ptr, const void* src, int64_t batch, int64_t length,
+                         int64_t segments, void* out, int lm, SmPlanSpace sp, const SmPlan& plan, bool binned) {
+  if (!binned) {
+    const dim3 grid((unsigned)((segments + 3) / 4), (unsigned)batch);
+    hipLaunchKernelGGL(row_softmax_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, out, lm,
+                       LongRowList{nullptr, nullptr});
+  } else if (plan.total > 0) {
+    const dim3 g((unsigned)((plan.total + 3) / 4), (unsigned)batch);
+    hipLaunchKernelGGL(row_softmax_binned_kernel<DT>, g, dim3(256), 0, st, src, length, out, lm, sp.rows, plan);
+  }
+  const int64_t nlong = plan.row_off[kSmClasses] - plan.row_off[kSmClasses - 1];
+  if (nlong > 0) {
+    // long rows from their kept bounds, batch = blockIdx.y
+    LongRowList list{sp.counts + (kSmClasses - 1), nullptr};
+    const dim3 g((unsigned)std::min<int64_t>(nlong, 4096), (unsigned)batch);
+    hipLaunchKernelGGL(row_softmax_long_kernel<DT>, g, dim3(256), 0, st, ptr, src, length, segments, out, lm, list,
+                       sp.rows + plan.row_off[kSmClasses - 1]);
+  }
+}
+
+template <int DT>
+void build_softmax_plan(hipStream_t st, const int64_t* ptr, int64_t length, int64_t segments, SmPlanSpace sp) {
+  const unsigned blocks = (unsigned)((segments + 255) / 256);
+  hipLaunchKernelGGL(sm_zero_kernel, dim3(1), dim3(64), 0, st, sp.counts, 2 * kSmClasses);
+  hipLaunchKernelGGL(sm_plan_count_kernel<DT>, dim3(blocks), dim3(256), 0, st, ptr, length, segments, sp.counts);
+  hipLaunchKernelGGL(sm_plan_scan_kernel, dim3(1), dim3(64), 0, st, sp.counts, sp.cursor);
+  hipLaunchKernelGGL(sm_plan_scatter_kernel<DT>, dim3(blocks), dim3(256), 0, st, ptr, length, segments, sp.cursor,
+                     sp.rows);
+}
+
 template <int DT>
 void launch_softmax_rows(dim3 grid, hipStream_t st, const int64_t* ptr, const void* src, int64_t length,
                          int64_t segments, void* out, int lm, LongRowList list, int64_t capacity) {
@@ -532,7 +810,7 @@ void launch_softmax_rows(dim3 grid, hipStream_t st, const int64_t* ptr, const vo
   hipLaunchKernelGGL(row_softmax_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, out, lm, list);
   const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(capacity, 4096));
   hipLaunchKernelGGL(row_softmax_long_kernel<DT>, dim3(blocks), dim3(256), 0, st, ptr, src, length, segments, out,
-                     lm, list);
+                     lm, list, nullptr);
 }
 
 void launch_stats_rows(int dtype, int64_t batch, hipStream_t st, const int64_t* ptr, const void* src, int64_t length,
@@ -671,15 +949,21 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
              static_cast<hipStream_t>(stream), "segment_stats");
 }
 
+// Workspace: the long-row list (header + capacity), then the kept plan
+// (counts and cursors, 256 bytes, then 16 bytes of bounds per segment).
+static size_t softmax_list_bytes(int64_t batch, int64_t length, int64_t segments, int vec) {
+  return (kListHeader + sizeof(int64_t) * (size_t)long_row_capacity(batch, length, segments, vec) + 255) / 256 * 256;
+}
+
 size_t ogn_segment_group_softmax_workspace_size(int64_t batch, int64_t length, int64_t segments, int dtype) {
   if (batch <= 0 || length < 0 || segments < 0) return 0;
   const int vec = 16 / dtype_size(dtype);
-  return kListHeader + sizeof(int64_t) * (size_t)long_row_capacity(batch, length, segments, vec);
+  return softmax_list_bytes(batch, length, segments, vec) + 256 + sizeof(longlong2) * (size_t)segments;
 }
 
 int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
-                              int64_t segments, void* out, int log_softmax, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+                              int64_t segments, void* out, int log_softmax, int flags, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   if (batch < 0 || length < 0 || segments < 0) return fail(OGN_EINVAL, "ogn_segment_group_softmax: negative size");
   if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
     return fail(OGN_EUNSUPPORTED, "ogn_segment_group_softmax: src dtype must be float32, float16 or bfloat16");
@@ -700,9 +984,37 @@ int ogn_segment_group_softmax(const int64_t* indptr, const void* src, int dtype,
   TimedLaunch t("segment_softmax", st);
   const dim3 grid((unsigned)((segments + 3) / 4), (unsigned)batch);
   const int lm = log_softmax ? 1 : 0;
+  char* plan_base = static_cast<char*>(workspace) + softmax_list_bytes(batch, length, segments, vec);
+  SmPlanSpace sp{reinterpret_cast<unsigned long long*>(plan_base),
+                 reinterpret_cast<unsigned long long*>(plan_base) + kSmClasses,
+                 reinterpret_cast<longlong2*>(plan_base + 256)};
+  KeptKey key{workspace, indptr, {2, batch, length, segments, vec, 0, 0, 0}, {}};
+  int64_t counts[8];
+  if ((flags & OGN_SEG_REUSE_LAYOUT) && kept_layout_find(key, counts)) {
+    // the kept plan of this pointer array: rows binned by length
+    const SmPlan plan = sm_plan_from_counts(counts);
+    const bool bn = sm_plan_binned(counts);
+    if (dtype == OGN_F32) launch_softmax_plan<OGN_F32>(st, indptr, src, batch, length, segments, out, lm, sp, plan, bn);
+    else if (dtype == OGN_F16) launch_softmax_plan<OGN_F16>(st, indptr, src, batch, length, segments, out, lm, sp, plan, bn);
+    else launch_softmax_plan<OGN_BF16>(st, indptr, src, batch, length, segments, out, lm, sp, plan, bn);
+    return check_launch("ogn_segment_group_softmax");
+  }
   if (dtype == OGN_F32) launch_softmax_rows<OGN_F32>(grid, st, indptr, src, length, segments, out, lm, list, capacity);
   else if (dtype == OGN_F16) launch_softmax_rows<OGN_F16>(grid, st, indptr, src, length, segments, out, lm, list, capacity);
   else launch_softmax_rows<OGN_BF16>(grid, st, indptr, src, length, segments, out, lm, list, capacity);
+  if (flags & (OGN_SEG_KEEP_LAYOUT | OGN_SEG_REUSE_LAYOUT)) {
+    // build the plan for later calls: four small kernels and one 64-byte
+    // read of the class counts (this call waits for it)
+    if (dtype == OGN_F32) build_softmax_plan<OGN_F32>(st, indptr, length, segments, sp);
+    else if (dtype == OGN_F16) build_softmax_plan<OGN_F16>(st, indptr, length, segments, sp);
+    else build_softmax_plan<OGN_BF16>(st, indptr, length, segments, sp);
+    unsigned long long host[kSmClasses];
+    if (hipMemcpyAsync(host, sp.counts, sizeof(host), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+      return fail(OGN_EHIP, "ogn_segment_group_softmax: reading the row-class counts failed");
+    for (int c = 0; c < kSmClasses; ++c) key.payload[c] = (int64_t)host[c];
+    kept_layout_store(key);
+  }
   return check_launch("ogn_segment_group_softmax");
 }
 

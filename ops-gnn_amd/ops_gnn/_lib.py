@@ -73,7 +73,7 @@ SIGNATURES = {
     "ogn_index_facts": (_int, [_vp, _i64, _vp, _vp]),
     "ogn_segment_group_stats": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "ogn_segment_group_softmax_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
-    "ogn_segment_group_softmax": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _int, _vp, _sz, _vp]),
+    "ogn_segment_group_softmax": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _int, _int, _vp, _sz, _vp]),
     "ogn_scatter_atomic_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
     "ogn_scatter_atomic": (_int, [_vp, _int, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _int,
                                   _int, _vp, _sz, _vp]),

@@ -295,16 +295,23 @@ def fused_row_softmax_ok(src3: torch.Tensor, groups: int) -> bool:
             and (b == 1 or (length * src3.element_size()) % 16 == 0) and b <= 65535)
 
 
-def group_softmax_rows(src3: torch.Tensor, ptr: torch.Tensor, groups: int, log_softmax: bool) -> torch.Tensor:
+def group_softmax_rows(src3: torch.Tensor, ptr: torch.Tensor, groups: int, log_softmax: bool,
+                       key: Optional[torch.Tensor] = None) -> torch.Tensor:
     b, length, _ = src3.shape
     out = torch.empty_like(src3)
     if out.numel() == 0:
         return out
     code = _lib.TORCH_TO_OGN[src3.dtype]
     ws_bytes = lib.ogn_segment_group_softmax_workspace_size(b, length, groups, code)
-    ws = _lib.workspace(ws_bytes, src3.device)
+    stream = stream_of(src3)
+    if key is not None and ws_bytes <= _LAYOUT_WS_MAX_BYTES:
+        # a kept row plan: later calls with this pointer tensor bin the rows
+        sub = ("softmax", ptr.data_ptr(), b, length, groups, code, stream.value, ws_bytes)
+        ws, flags = _layout_workspace(key, sub, ws_bytes, src3.device)
+    else:
+        ws, flags = _lib.workspace(ws_bytes, src3.device), 0
     rc = lib.ogn_segment_group_softmax(dptr(ptr), dptr(src3), code, b, length, groups, dptr(out),
-                                       1 if log_softmax else 0, dptr(ws), ws_bytes, stream_of(src3))
+                                       1 if log_softmax else 0, flags, dptr(ws), ws_bytes, stream)
     check(rc, "grouped softmax")
     return out
 

@@ -105,7 +105,8 @@ class _GroupedSoftmax(torch.autograd.Function):
         src3 = src.contiguous().reshape(shape3)
         if is_sorted and _native.fused_row_softmax_ok(src3, groups):
             # one feature per position, long rows: statistics and output in one pass per row
-            out3 = _native.group_softmax_rows(src3, _native.sorted_index_ptr(index, groups), groups, log_softmax)
+            ptr = _native.sorted_index_ptr(index, groups)
+            out3 = _native.group_softmax_rows(src3, ptr, groups, log_softmax, key=ptr)
         else:
             m, s = _stats(src3, index, groups, is_sorted)
             out3 = _native.group_softmax_apply(src3, index, groups, m, s, log_softmax)

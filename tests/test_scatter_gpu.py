@@ -257,6 +257,64 @@ def test_grouped_softmax_repeated_calls(ogn, oracle, dtype, mode, before):
                                    err_msg=f"call {step}")
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax"])
+@pytest.mark.parametrize("before", [1, 3])
+def test_grouped_softmax_binned_rows(ogn, oracle, dtype, mode, before):
+    # The first call bins the rows by packet count into a kept plan; later
+    # calls with the same index run them binned: 8 / 16 / 32-lane groups for
+    # rows of up to 8 / 16 / 32 packets (several rows per wavefront, the last
+    # wavefront of a class partly empty), one wavefront for up to 256 packets,
+    # a block beyond.  Sizes straddle every class edge at unaligned starts,
+    # with empty rows and +-inf / NaN in short rows.
+    v = 8 if dtype != torch.float32 else 4
+    edges = [8, 16, 32, 64, 128, 192, 256]
+    sizes = [0, 1, 2, v - 1, v + 1]
+    for e in edges:
+        sizes += [e * v - 3, e * v, e * v + 2]
+    sizes += [300 * v, 1500 * v + 5]
+    rng = np.random.default_rng(56)
+    deg = np.array([sizes[i] for i in rng.integers(0, len(sizes), 400)] + sizes, dtype=np.int64)
+    deg = np.maximum(deg, 0)
+    idx = np.repeat(np.arange(deg.size), deg)
+    x = (rng.standard_normal((before, idx.size)) * 4).astype(np.float32)
+    starts = np.concatenate([[0], np.cumsum(deg)])
+    short = [r for r in range(deg.size) if 2 <= deg[r] <= 8 * v][:3]
+    x[0, starts[short[0]]] = INF
+    x[-1, starts[short[1]] + 1] = NAN
+    x[0, starts[short[2]]: starts[short[2] + 1]] = -INF
+    src = torch.from_numpy(x).to(dtype)
+    index = torch.from_numpy(idx).cuda()
+    fn = ogn.scatter_softmax if mode == "softmax" else ogn.scatter_log_softmax
+    gold = cast_like(oracle.group_softmax(src, torch.from_numpy(idx), 1, deg.size, mode), dtype)
+    for step in range(3):
+        got = fn(src.cuda(), index, 1, deg.size).float().cpu().numpy()
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(gold), err_msg=f"call {step}")
+        np.testing.assert_allclose(got, gold, rtol=SOFT_TOL[dtype], atol=SOFT_TOL[dtype], equal_nan=True,
+                                   err_msg=f"call {step}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("before", [1, 2])
+def test_grouped_softmax_kept_plan_row_order(ogn, oracle, dtype, before):
+    # A kept plan with few short rows runs the rows one wavefront each in
+    # row order and takes its long rows (> 256 packets) from the plan's
+    # bounds, with no list-building launch.
+    v = 8 if dtype != torch.float32 else 4
+    rng = np.random.default_rng(57)
+    deg = rng.integers(33 * v, 256 * v, 300)
+    deg[::40] = rng.integers(257 * v, 900 * v, deg[::40].size)
+    deg[7] = 3
+    deg[8] = 0
+    idx = np.repeat(np.arange(deg.size), deg)
+    src = torch.from_numpy((rng.standard_normal((before, idx.size)) * 4).astype(np.float32)).to(dtype)
+    index = torch.from_numpy(idx).cuda()
+    gold = cast_like(oracle.group_softmax(src, torch.from_numpy(idx), 1, deg.size, "log_softmax"), dtype)
+    for step in range(3):
+        got = ogn.scatter_log_softmax(src.cuda(), index, 1, deg.size).float().cpu().numpy()
+        np.testing.assert_allclose(got, gold, rtol=SOFT_TOL[dtype], atol=SOFT_TOL[dtype], err_msg=f"call {step}")
+
+
 @pytest.mark.parametrize("sorted_index", [True, False])
 def test_grouped_softmax_special_values(ogn, oracle, sorted_index):
     src = torch.tensor([INF, 1.0, -INF, 2.0, NAN, 0.0, -INF, -INF])
