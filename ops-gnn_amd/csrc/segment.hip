@@ -424,6 +424,101 @@ __device__ __forceinline__ void block_row_in_registers(const typename Elem<DT>::
 // registers (8 loads in flight per thread); longer rows take two passes over
 // chunks of 256 * 8 packets (log-sum-exp statistics, then the outputs), each
 // chunk's 8 loads per thread issued together.
+// One long row, [rs, re) of `row`, over a 256-thread block: rows of up to
+// 256 * UB packets in registers (UB loads in flight per thread), longer rows
+// in two passes over chunks of 256 * UB packets (log-sum-exp statistics,
+// then the outputs), each chunk's UB loads per thread issued together.
+template <int DT, int UB>
+__device__ __forceinline__ void long_row_block(const typename Elem<DT>::S* __restrict__ row, void* __restrict__ out,
+                                               int64_t obase, int64_t rs, int64_t re, int64_t length, int log_mode,
+                                               float* red) {
+  using E = Elem<DT>;
+  constexpr int V = E::VEC;
+  constexpr int T = 256;
+  const int t = (int)threadIdx.x;
+  const int64_t q0 = rs / V * V;
+  const uint32_t n = (uint32_t)(re - rs);
+  const int64_t pk = row_packets<DT>(rs, re);
+  if (pk <= 2 * T) {
+    block_row_in_registers<DT, 2>(row, out, obase, rs, re, length, log_mode, red);
+  } else if (pk <= 4 * T) {
+    block_row_in_registers<DT, 4>(row, out, obase, rs, re, length, log_mode, red);
+  } else if (pk <= (int64_t)UB * T) {
+    block_row_in_registers<DT, UB>(row, out, obase, rs, re, length, log_mode, red);
+  } else {
+    // statistics: per-thread online (m, s) over chunks, then block max and
+    // rescaled sum
+    constexpr int64_t kChunk = (int64_t)UB * T * V;
+    float m = -__builtin_inff(), sacc = 0.f;
+    for (int64_t c0 = q0; c0 < re; c0 += kChunk) {
+      uint4 raw[UB];
+#pragma unroll
+      for (int u = 0; u < UB; ++u)
+        raw[u] = load16(row + packet_address<DT>(c0 + (int64_t)(u * T + t) * V, q0, re, length));
+      float pm = m;
+      float x[UB][V];
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+        const int64_t q = c0 + (int64_t)(u * T + t) * V;
+        if (q < re && q + V > length) {
+#pragma unroll
+          for (int i = 0; i < V; ++i) x[u][i] = q + i < length ? E::load1(row, q + i) : 0.f;
+        } else {
+          E::unpack(raw[u], x[u]);
+        }
+        const int64_t d = q - rs;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          x[u][i] = (uint64_t)(d + i) < (uint64_t)n ? x[u][i] : -__builtin_inff();
+          pm = fmaxf(pm, x[u][i]);
+        }
+      }
+      const float cn = clampf_max(pm);
+      float acc = sacc * fast_exp(clampf_max(m) - cn);
+#pragma unroll
+      for (int u = 0; u < UB; ++u)
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc += fast_exp(x[u][i] - cn);
+      m = pm;
+      sacc = acc;
+    }
+    const float gm = block_reduce256<true>(m, red);
+    const float sv = sacc == 0.f ? 0.f : sacc * fast_exp(clampf_max(m) - clampf_max(gm));
+    const float s = block_reduce256<false>(sv, red);
+    const float cm = clampf_max(gm);
+    float inv, ls;
+    softmax_row_constants(gm, s, inv, ls);
+    for (int64_t c0 = q0; c0 < re; c0 += kChunk) {
+      uint4 raw[UB];
+#pragma unroll
+      for (int u = 0; u < UB; ++u)
+        raw[u] = load16(row + packet_address<DT>(c0 + (int64_t)(u * T + t) * V, q0, re, length));
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+        const int64_t q = c0 + (int64_t)(u * T + t) * V;
+        if (q >= re) continue;
+        float x[V], v[V];
+        if (q + V > length) {
+#pragma unroll
+          for (int i = 0; i < V; ++i) x[i] = q + i < length ? E::load1(row, q + i) : 0.f;
+        } else {
+          E::unpack(raw[u], x);
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = log_mode ? (x[i] - cm) - ls : fast_exp(x[i] - cm) * inv;
+        const int64_t d = q - rs;
+        if (d >= 0 && d + V <= (int64_t)n) {
+          store_floats<V, true>(out, DT, obase + q, v);
+        } else {
+#pragma unroll
+          for (int i = 0; i < V; ++i)
+            if ((uint64_t)(d + i) < (uint64_t)n) store_floats<1>(out, DT, obase + q + i, &v[i]);
+        }
+      }
+    }
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void row_softmax_long_kernel(const int64_t* __restrict__ ptr,
                                                                const void* __restrict__ src, int64_t length,
@@ -431,11 +526,7 @@ __global__ __launch_bounds__(256) void row_softmax_long_kernel(const int64_t* __
                                                                int log_mode, LongRowList list,
                                                                const longlong2* __restrict__ bounds) {
   using E = Elem<DT>;
-  constexpr int V = E::VEC;
-  constexpr int UB = 8;
-  constexpr int T = 256;
   __shared__ float red[4];
-  const int t = (int)threadIdx.x;
   const int64_t count = (int64_t)*list.count;
   for (int64_t item = blockIdx.x; item < count; item += gridDim.x) {
     // a row code b * segments + r of the list, or (bounds given: a kept
@@ -453,89 +544,8 @@ __global__ __launch_bounds__(256) void row_softmax_long_kernel(const int64_t* __
       rs = std::max<int64_t>(ptr[r], 0);
       re = std::min<int64_t>(ptr[r + 1], length);
     }
-    const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
-    const int64_t obase = b * length;
-    const int64_t q0 = rs / V * V;
-    const uint32_t n = (uint32_t)(re - rs);
-    const int64_t pk = row_packets<DT>(rs, re);
-    if (pk <= 2 * T) {
-      block_row_in_registers<DT, 2>(row, out, obase, rs, re, length, log_mode, red);
-    } else if (pk <= 4 * T) {
-      block_row_in_registers<DT, 4>(row, out, obase, rs, re, length, log_mode, red);
-    } else if (pk <= (int64_t)UB * T) {
-      block_row_in_registers<DT, UB>(row, out, obase, rs, re, length, log_mode, red);
-    } else {
-      // statistics: per-thread online (m, s) over chunks, then block max and
-      // rescaled sum
-      constexpr int64_t kChunk = (int64_t)UB * T * V;
-      float m = -__builtin_inff(), sacc = 0.f;
-      for (int64_t c0 = q0; c0 < re; c0 += kChunk) {
-        uint4 raw[UB];
-#pragma unroll
-        for (int u = 0; u < UB; ++u)
-          raw[u] = load16(row + packet_address<DT>(c0 + (int64_t)(u * T + t) * V, q0, re, length));
-        float pm = m;
-        float x[UB][V];
-#pragma unroll
-        for (int u = 0; u < UB; ++u) {
-          const int64_t q = c0 + (int64_t)(u * T + t) * V;
-          if (q < re && q + V > length) {
-#pragma unroll
-            for (int i = 0; i < V; ++i) x[u][i] = q + i < length ? E::load1(row, q + i) : 0.f;
-          } else {
-            E::unpack(raw[u], x[u]);
-          }
-          const int64_t d = q - rs;
-#pragma unroll
-          for (int i = 0; i < V; ++i) {
-            x[u][i] = (uint64_t)(d + i) < (uint64_t)n ? x[u][i] : -__builtin_inff();
-            pm = fmaxf(pm, x[u][i]);
-          }
-        }
-        const float cn = clampf_max(pm);
-        float acc = sacc * fast_exp(clampf_max(m) - cn);
-#pragma unroll
-        for (int u = 0; u < UB; ++u)
-#pragma unroll
-          for (int i = 0; i < V; ++i) acc += fast_exp(x[u][i] - cn);
-        m = pm;
-        sacc = acc;
-      }
-      const float gm = block_reduce256<true>(m, red);
-      const float sv = sacc == 0.f ? 0.f : sacc * fast_exp(clampf_max(m) - clampf_max(gm));
-      const float s = block_reduce256<false>(sv, red);
-      const float cm = clampf_max(gm);
-      float inv, ls;
-      softmax_row_constants(gm, s, inv, ls);
-      for (int64_t c0 = q0; c0 < re; c0 += kChunk) {
-        uint4 raw[UB];
-#pragma unroll
-        for (int u = 0; u < UB; ++u)
-          raw[u] = load16(row + packet_address<DT>(c0 + (int64_t)(u * T + t) * V, q0, re, length));
-#pragma unroll
-        for (int u = 0; u < UB; ++u) {
-          const int64_t q = c0 + (int64_t)(u * T + t) * V;
-          if (q >= re) continue;
-          float x[V], v[V];
-          if (q + V > length) {
-#pragma unroll
-            for (int i = 0; i < V; ++i) x[i] = q + i < length ? E::load1(row, q + i) : 0.f;
-          } else {
-            E::unpack(raw[u], x);
-          }
-#pragma unroll
-          for (int i = 0; i < V; ++i) v[i] = log_mode ? (x[i] - cm) - ls : fast_exp(x[i] - cm) * inv;
-          const int64_t d = q - rs;
-          if (d >= 0 && d + V <= (int64_t)n) {
-            store_floats<V, true>(out, DT, obase + q, v);
-          } else {
-#pragma unroll
-            for (int i = 0; i < V; ++i)
-              if ((uint64_t)(d + i) < (uint64_t)n) store_floats<1>(out, DT, obase + q + i, &v[i]);
-          }
-        }
-      }
-    }
+    long_row_block<DT, 8>(static_cast<const typename E::S*>(src) + b * length, out, b * length, rs, re, length,
+                          log_mode, red);
   }
 }
 
@@ -572,7 +582,8 @@ struct SmPlan {
   int64_t row_off[kSmClasses + 1];  // class c's rows: rows[row_off[c] .. row_off[c + 1])
   int64_t wave_off[kSmPacked];      // first wavefront of class c in the binned launch
   int64_t waves[kSmPacked];         // wavefronts of class c
-  int64_t total;                    // wavefronts of the binned launch
+  int64_t total;                    // wavefronts of the classes above
+  int64_t long_blocks;              // leading blocks of the launch: one per long row
 };
 
 // Binning pays when short rows are common: with fewer than 1/8 of the rows
@@ -599,6 +610,7 @@ SmPlan sm_plan_from_counts(const int64_t* counts) {
     w += pl.waves[c];
   }
   pl.total = w;
+  pl.long_blocks = counts[kSmClasses - 1];
   return pl;
 }
 
@@ -747,16 +759,23 @@ __global__ __launch_bounds__(256) void row_softmax_binned_kernel(const void* __r
                                                                  void* __restrict__ out, int log_mode,
                                                                  const longlong2* __restrict__ rows, SmPlan plan) {
   using E = Elem<DT>;
-  const int64_t w = (int64_t)blockIdx.x * 4 + wave_in_block();
+  __shared__ float red[4];
+  const int64_t b = blockIdx.y;
+  const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
+  const int64_t obase = b * length;
+  if ((int64_t)blockIdx.x < plan.long_blocks) {
+    // the long rows lead the grid, a block each (up to 1024 packets in
+    // registers, two passes beyond), so that they overlap the rest
+    const longlong2 bd = rows[plan.row_off[kSmClasses - 1] + blockIdx.x];
+    return long_row_block<DT, 4>(row, out, obase, bd.x, bd.y, length, log_mode, red);
+  }
+  const int64_t w = ((int64_t)blockIdx.x - plan.long_blocks) * 4 + wave_in_block();
   if (w >= plan.total) return;
   int c = 0;
 #pragma unroll
   for (int k = 0; k < kSmPacked; ++k)
     if (w >= plan.wave_off[k] && w < plan.wave_off[k] + plan.waves[k]) c = k;
   const int64_t idx = w - plan.wave_off[c];
-  const int64_t b = blockIdx.y;
-  const typename E::S* row = static_cast<const typename E::S*>(src) + b * length;
-  const int64_t obase = b * length;
   const int64_t first = plan.row_off[c] + idx * sm_rows_per_wave(c), last = plan.row_off[c + 1];
   switch (c) {
     case 0: return binned_groups<DT, 8>(row, out, obase, length, log_mode, rows, first, last);
@@ -779,9 +798,12 @@ void launch_softmax_plan(hipStream_t st, const int64_t* ptr, const void* src, in
     const dim3 grid((unsigned)((segments + 3) / 4), (unsigned)batch);
     hipLaunchKernelGGL(row_softmax_k1_kernel<DT>, grid, dim3(256), 0, st, ptr, src, length, segments, out, lm,
                        LongRowList{nullptr, nullptr});
-  } else if (plan.total > 0) {
-    const dim3 g((unsigned)((plan.total + 3) / 4), (unsigned)batch);
-    hipLaunchKernelGGL(row_softmax_binned_kernel<DT>, g, dim3(256), 0, st, src, length, out, lm, sp.rows, plan);
+  } else {
+    if (plan.total + plan.long_blocks > 0) {
+      const dim3 g((unsigned)(plan.long_blocks + (plan.total + 3) / 4), (unsigned)batch);
+      hipLaunchKernelGGL(row_softmax_binned_kernel<DT>, g, dim3(256), 0, st, src, length, out, lm, sp.rows, plan);
+    }
+    return;
   }
   const int64_t nlong = plan.row_off[kSmClasses] - plan.row_off[kSmClasses - 1];
   if (nlong > 0) {
