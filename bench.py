@@ -518,7 +518,10 @@ def bench_gat(args):
             log(f"bench gat {name}: {ms:.4f} ms, effective {eff[name] / ms / 1e6:.1f} GB/s, "
                 f"compulsory {comp[name] / ms / 1e6:.1f} GB/s")
         ms = _timed(layer, args.steps, args.warmup)
-        km = _kernel_ms(layer, args.steps, ["sddmm_main", "spmm_main", "segment_softmax", "group_apply", "segment_stats_main"])
+        km = _kernel_ms(layer, args.steps, ["sddmm_main", "spmm_main", "sddmm_xcd", "spmm_xcd", "spmm_xcd_combine",
+                                            "segment_softmax", "group_apply", "segment_stats_main"])
+        # the XCD-tiled kernels replace sddmm_main / spmm_main when the graph and table sizes select them
+        sddmm_kernel = "sddmm_xcd" if km["sddmm_xcd"] > 0 else "sddmm_main"
         gfloor = gather_floor_ms(kk, col)
         log(f"bench gat: gathering the {e} K rows alone {gfloor:.3f} ms")
     tot_eff = sum(eff.values())
@@ -540,7 +543,7 @@ def bench_gat(args):
                "sample": f"oracle_sddmm dot (C) on rows [0, {r}) = {int(ptr_np[r])} edges, {dt:.2f} s"}
     return _line("GAT layer (sddmm + scatter_softmax + SpMM) effective GB/s (config 4)", tot_eff / ms / 1e6,
                  "GB/s", ms, args, "f16", "configs[3]: GAT-style attention layer",
-                 {"nodes": n, "nnz": e, "k": f}, ops, "sddmm_main", comp["sddmm"], km["sddmm_main"], cpu,
+                 {"nodes": n, "nnz": e, "k": f}, ops, sddmm_kernel, comp["sddmm"], km[sddmm_kernel], cpu,
                  basis="compulsory: col + scores + Q and K read once (the per-edge K-row gathers hit the "
                        "256 MB MALL, since K is 29.8 MB)")
 

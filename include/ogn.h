@@ -394,6 +394,37 @@ int ogn_gather_csr(const int64_t* indptr, int64_t ptr_batches, const void* src, 
 int ogn_gather_coo(const int64_t* index, const void* src, int64_t batch, int64_t src_rows, int64_t entries,
                    int64_t row_bytes, void* out, void* stream);
 
+/* ------------------------------------------------------------------ XCD tiles
+ * Column-tiled SDDMM dot and SpMM sum, for graphs whose gathered feature
+ * table is larger than one XCD's 4 MB L2 but small enough that an eighth of
+ * it fits (the 29.8 MB K / V of an attention layer).  Workgroup b runs on XCD
+ * b % 8 and gathers only columns of tile b % 8, so its rows stay in that
+ * XCD's L2.  No counterpart in the reference (its kernels have no cache
+ * tiers to target); results: SDDMM bit-identical to ogn_sddmm_csr's dot, SpMM
+ * the same sum in another order (per-tile fp32 partials, added in tile
+ * order: deterministic).
+ * ogn_xcd_plan: builds the plan of (rowptr, col) into `plan`
+ *   (ogn_xcd_plan_bytes bytes): row-aligned chunks of about 8192 edges and,
+ *   for every row, where each of 8 column tiles (n_cols / 8 columns wide)
+ *   starts in its edge range.  *sorted = 1 when every row's columns are
+ *   sorted (only then do the tiles follow column ranges; the results are
+ *   right either way).  Waits for a 4-byte read.  Fewer than 2^31 edges.
+ * ogn_sddmm_dot_xcd: out[e] = dot(lhs[row(e)], rhs[col[e]]) (lhs_target =
+ *   row, rhs_target = col), k * element size 64, 128, 256 or 512 bytes.
+ * ogn_spmm_sum_xcd: out[r] = sum_e value[e] * mat[col[e]] (one weight per
+ *   edge, batch 1), out dtype = mat dtype or float32; workspace
+ *   ogn_spmm_sum_xcd_workspace_size(m, k) bytes (8 fp32 partial outputs). */
+size_t ogn_xcd_plan_bytes(int64_t m, int64_t nnz);
+int ogn_xcd_plan(const void* rowptr, const void* col, int index_dtype, int64_t m, int64_t n_cols, int64_t nnz,
+                 void* plan, size_t plan_bytes, int* sorted, void* stream);
+int ogn_sddmm_dot_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, int index_dtype, const void* lhs,
+                      int64_t lhs_rows, const void* rhs, int64_t rhs_rows, int64_t k, int dtype, void* out,
+                      void* stream);
+size_t ogn_spmm_sum_xcd_workspace_size(int64_t m, int64_t k);
+int ogn_spmm_sum_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, int index_dtype, const void* value,
+                     const void* mat, int64_t n, int64_t k, int dtype, void* out, int out_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ measurement
  * Practical memory ceilings, reported by bench.py beside the 8 TB/s HBM
  * peak.  No counterpart in the reference; they serve measurement only.

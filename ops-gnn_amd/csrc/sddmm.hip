@@ -11,6 +11,7 @@
 // row-index array in memory).  dot is reduced across the G lanes of a
 // sub-group with ds_bpermute.  fp16 / bf16 compute in fp32 and round once.
 #include "csr_engine.h"
+#include "dot.h"
 
 #include <string>
 
@@ -217,46 +218,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
 // rows DPP permutes do it without the LDS unit: xor 1 and xor 2 by quad
 // permutation, then the half-row and row mirrors pair each lane with one in
 // the other half; wider groups add swizzle / bpermute rounds.
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-  auto dpp = [](float x, auto ctrl) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
-  };
-  if constexpr (G >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
-  if constexpr (G >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
-  if constexpr (G >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
-  if constexpr (G >= 16) v += dpp(v, std::integral_constant<int, 0x140>{}); // row_mirror
-  if constexpr (G >= 32) v += xor_shfl<16>(v);
-  if constexpr (G >= 64) v += xor_shfl<32>(v);
-  return v;
-}
 
-// Dot of two 16-byte feature packets, accumulated in fp32: fp16 and bf16
-// pairs go through v_dot2c_f32_f16 / v_dot2c_f32_bf16 (products of 16-bit
-// values are exact in fp32), four instructions per packet; fp32 packets take
-// four FMAs.
-template <int DT>
-__device__ __forceinline__ float packet_dot(const uint4& a, const uint4& b, float d) {
-  if constexpr (DT == OGN_F16) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.x), __builtin_bit_cast(h2, b.x), d, false);
-    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.y), __builtin_bit_cast(h2, b.y), d, false);
-    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.z), __builtin_bit_cast(h2, b.z), d, false);
-    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a.w), __builtin_bit_cast(h2, b.w), d, false);
-  } else if constexpr (DT == OGN_BF16) {
-    typedef short s2 __attribute__((ext_vector_type(2)));
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.x), __builtin_bit_cast(s2, b.x), d, false);
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.y), __builtin_bit_cast(s2, b.y), d, false);
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.z), __builtin_bit_cast(s2, b.z), d, false);
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2, a.w), __builtin_bit_cast(s2, b.w), d, false);
-  } else {
-    d = __builtin_fmaf(__uint_as_float(a.x), __uint_as_float(b.x), d);
-    d = __builtin_fmaf(__uint_as_float(a.y), __uint_as_float(b.y), d);
-    d = __builtin_fmaf(__uint_as_float(a.z), __uint_as_float(b.z), d);
-    d = __builtin_fmaf(__uint_as_float(a.w), __uint_as_float(b.w), d);
-  }
-  return d;
-}
 
 // dot(lhs[row(e)], rhs[col(e)]) -- the GAT score and the SpMM edge-weight
 // gradient.  Specialises the generic kernel for that case: the lhs row is

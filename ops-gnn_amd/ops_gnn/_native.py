@@ -92,6 +92,9 @@ def spmm_forward(ptr: torch.Tensor, col: torch.Tensor, value: Optional[torch.Ten
     arg = torch.empty(shape if minmax else (0,), dtype=torch.int64, device=mat.device)
     if out.numel() == 0:
         return out, arg
+    if reduce == _lib.R_SUM and batch == 1 and width == 1 and out.is_contiguous() and \
+            spmm_sum_xcd(ptr, col, value, mat.view(n, k), out):
+        return out, arg
     ws_bytes = lib.ogn_spmm_csr_workspace_size(m, nnz, k, batch, _lib.TORCH_TO_OGN[mat.dtype], reduce)
     ws = _lib.workspace(ws_bytes, mat.device)
     rc = lib.ogn_spmm_csr(dptr(ptr), dptr(col), _index_code(ptr), dptr(value), width, dptr(mat),
@@ -100,6 +103,91 @@ def spmm_forward(ptr: torch.Tensor, col: torch.Tensor, value: Optional[torch.Ten
                           dptr(ws), ws_bytes, stream_of(mat))
     check(rc, "spmm")
     return out, arg
+
+
+# ------------------------------------------------------------------ XCD tiles
+# Column-tiled SDDMM dot / SpMM sum (include/ogn.h, ogn_xcd_*): used when the
+# gathered table is larger than one XCD's L2 and an eighth of it fits (8-96 MB),
+# on graphs of at least 2^20 edges.  OGN_XCD=0 turns the path off, OGN_XCD=1
+# takes it whenever the row width allows (tests).
+XCD_TABLE_BYTES = (8 << 20, 96 << 20)
+XCD_MIN_EDGES = 1 << 20
+_XCD_PLANS = None
+
+
+def xcd_wanted(table_rows: int, row_bytes: int, nnz: int) -> bool:
+    import os
+
+    mode = os.environ.get("OGN_XCD", "")
+    if mode == "0" or row_bytes not in (64, 128, 256, 512) or not 0 < nnz < (1 << 31):
+        return False
+    if mode == "1":
+        return True
+    return XCD_TABLE_BYTES[0] <= table_rows * row_bytes <= XCD_TABLE_BYTES[1] and nnz >= XCD_MIN_EDGES
+
+
+def xcd_plan(ptr: torch.Tensor, col: torch.Tensor, n_cols: int) -> Optional[torch.Tensor]:
+    """The kept XCD plan of (ptr, col), or None when a row's columns are not
+    sorted (the tiles would not follow column ranges).  Cached per version of
+    col, together with ptr's address, version and n_cols."""
+    import ctypes
+
+    global _XCD_PLANS
+    if _XCD_PLANS is None:
+        _XCD_PLANS = _VersionCache(limit=8)
+    per_col = _XCD_PLANS.get(col, dict)
+    info = (ptr.data_ptr(), ptr._version, tuple(ptr.shape), ptr.dtype, n_cols)
+    hit = per_col.get(info)
+    if hit is None:
+        m, nnz = ptr.numel() - 1, col.numel()
+        plan = _lib.workspace(lib.ogn_xcd_plan_bytes(m, nnz), col.device)
+        sorted_flag = ctypes.c_int(0)
+        check(lib.ogn_xcd_plan(dptr(ptr), dptr(col), _index_code(ptr), m, n_cols, nnz, dptr(plan), plan.numel(),
+                               ctypes.byref(sorted_flag), stream_of(col)), "xcd plan")
+        hit = (plan, sorted_flag.value == 1)
+        per_col.clear()
+        per_col[info] = hit
+    return hit[0] if hit[1] else None
+
+
+def sddmm_dot_xcd(ptr, col, lhs, rhs, out) -> bool:
+    """dot(lhs[row], rhs[col]) into out through the XCD path; False when the
+    path does not apply (the caller runs ogn_sddmm_csr)."""
+    k = lhs.size(1)
+    nnz = col.numel()
+    if lhs.dtype not in SEGMENT_DTYPES or not xcd_wanted(rhs.size(0), k * lhs.element_size(), nnz):
+        return False
+    if lhs.data_ptr() % 16 or rhs.data_ptr() % 16 or ptr.dtype != col.dtype:
+        return False
+    plan = xcd_plan(ptr, col, rhs.size(0))
+    if plan is None:
+        return False
+    check(lib.ogn_sddmm_dot_xcd(dptr(plan), ptr.numel() - 1, nnz, dptr(col), _index_code(ptr), dptr(lhs),
+                                lhs.size(0), dptr(rhs), rhs.size(0), k, _lib.TORCH_TO_OGN[lhs.dtype], dptr(out),
+                                stream_of(lhs)), "sddmm_csr (xcd)")
+    return True
+
+
+def spmm_sum_xcd(ptr, col, value, mat, out) -> bool:
+    """out = A @ mat (sum, one weight per edge, batch 1) through the XCD path;
+    False when the path does not apply."""
+    m, nnz = ptr.numel() - 1, col.numel()
+    n, k = mat.shape
+    if mat.dtype not in SEGMENT_DTYPES or out.dtype not in (mat.dtype, torch.float32):
+        return False
+    if value is None or value.dtype != mat.dtype or value.numel() != nnz:
+        return False
+    if not xcd_wanted(n, k * mat.element_size(), nnz) or mat.data_ptr() % 16 or out.data_ptr() % 16:
+        return False
+    plan = xcd_plan(ptr, col, n)
+    if plan is None:
+        return False
+    ws_bytes = lib.ogn_spmm_sum_xcd_workspace_size(m, k)
+    ws = _lib.workspace(ws_bytes, mat.device)
+    check(lib.ogn_spmm_sum_xcd(dptr(plan), m, nnz, dptr(col), _index_code(ptr), dptr(value), dptr(mat), n, k,
+                               _lib.TORCH_TO_OGN[mat.dtype], dptr(out), _lib.TORCH_TO_OGN[out.dtype], dptr(ws),
+                               ws_bytes, stream_of(mat)), "spmm (xcd)")
+    return True
 
 
 # ------------------------------------------------------------------ segment engine

@@ -167,6 +167,8 @@ def sddmm_csr(indptr: torch.Tensor, indices: torch.Tensor, lhs: Optional[torch.T
     r2c = r2.contiguous() if use_r else None
     ptr = indptr.contiguous()
     col = indices.contiguous()
+    if is_dot and lt == 0 and rt == 2 and _native.sddmm_dot_xcd(ptr, col, l2c, r2c, result):
+        return result
     ws_bytes = lib.ogn_sddmm_csr_workspace_size(nnz, k, _lib.TORCH_TO_OGN[feature.dtype])
     ws = _lib.workspace(ws_bytes, feature.device)
     rc = lib.ogn_sddmm_csr(dptr(ptr), dptr(col), _lib.I64 if ptr.dtype == torch.int64 else _lib.I32, ptr.numel() - 1,

@@ -38,7 +38,7 @@ import weakref
 
 import torch
 
-from . import _native
+from . import _lib, _native
 from . import _pybind
 
 _C = _pybind.torch_sparse_spmm
@@ -278,7 +278,7 @@ class _SpmmFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, value, mat, csr, reduce, out_code):
-        out, arg = _C.forward(csr.ptr, csr.col, value, mat, reduce, out_code)
+        out, arg = _forward(csr.ptr, csr.col, value, mat, reduce, out_code)
         ctx.csr, ctx.reduce = csr, reduce
         ctx.value_shape = None if value is None else value.shape
         ctx.save_for_backward(value, mat, arg)
@@ -343,11 +343,27 @@ def _extremum_backward(csr, value, mat, arg, grad, want_v, want_m):
     return d_value, d_mat
 
 
+def _forward(ptr, col, value, mat, reduce: int, out_code: int):
+    """``_C.forward``, or for a weighted sum over one 2-D operand the
+    XCD-tiled SpMM when the graph and table sizes call for it
+    (``_native.spmm_sum_xcd``; include/ogn.h ogn_spmm_sum_xcd)."""
+    if reduce == 0 and mat.dim() == 2 and value is not None and value.dim() == 1 and col.dtype == ptr.dtype:
+        out_dtype = _OUT_DTYPES.get(out_code)
+        if out_dtype is not None and mat.dtype in _native.SEGMENT_DTYPES and out_dtype in (mat.dtype, torch.float32):
+            out = torch.empty((ptr.numel() - 1, mat.size(1)), dtype=out_dtype, device=mat.device)
+            if _native.spmm_sum_xcd(ptr.contiguous(), col.contiguous(), value.contiguous(), mat.contiguous(), out):
+                return out, torch.empty(0, dtype=torch.int64, device=mat.device)
+    return _C.forward(ptr, col, value, mat, reduce, out_code)
+
+
+_OUT_DTYPES = {code: dt for dt, code in _lib.TORCH_TO_OGN.items()}
+
+
 def _run(csr: _Csr, value, mat, reduce: int, out_code: int):
     """(out, arg) through autograd when a gradient is wanted, else directly."""
     if torch.is_grad_enabled() and (mat.requires_grad or (value is not None and value.requires_grad)):
         return _SpmmFunction.apply(value, mat, csr, reduce, out_code)
-    return _C.forward(csr.ptr, csr.col, value, mat, reduce, out_code)
+    return _forward(csr.ptr, csr.col, value, mat, reduce, out_code)
 
 
 def _prove_and_run(csr: _Csr, value, mat, reduce: int, output_dtype=None, required_metadata=False):
