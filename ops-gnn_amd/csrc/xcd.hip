@@ -179,7 +179,7 @@ void sddmm_dot_xcd_kernel(XcdArgs a) {
   constexpr int NE = E::VEC;
   constexpr int S = kWave / G;
   constexpr int NSTEPS = kWave / S;
-  constexpr int U = NSTEPS < 8 ? NSTEPS : 8;
+  constexpr int U = NSTEPS < 4 ? NSTEPS : 4;  // L2-hit gathers: 4 steps in flight, more waves
   const int lane = lane_id();
   const int sub = lane / G;
   const int gl = lane % G;
@@ -203,7 +203,7 @@ void sddmm_dot_xcd_kernel(XcdArgs a) {
       const int nw = std::min<int32_t>(kWave, w.total - vb);
       const int kl = row_of(w.incl, std::min<int32_t>(v, w.total - 1));
       const int64_t e = v + shfl64(w.d, kl);
-      const int32_t cl = v < w.total ? (int32_t)std::min<int64_t>(std::max<int64_t>(col[e], 0), a.rhs_rows - 1) : 0;
+      const int32_t cl = v < w.total ? (int32_t)std::min<int64_t>(std::max<int64_t>((int64_t)load_stream(col + e), 0), a.rhs_rows - 1) : 0;
       float mine = 0.f;
       for (int j0 = 0; j0 < NSTEPS; j0 += U) {
         uint4 xr[U];
@@ -228,7 +228,7 @@ void sddmm_dot_xcd_kernel(XcdArgs a) {
       // lane s * G + j holds the score of window position j * S + s
       const int pmine = gl * S + sub;
       const int64_t emine = shfl64(e, pmine);
-      if (pmine < nw) store_floats<1>(a.out, a.dt, emine, &mine);
+      if (pmine < nw) store_floats<1, true>(a.out, a.dt, emine, &mine);
     }
   }
 }
@@ -242,7 +242,7 @@ void spmm_sum_xcd_kernel(XcdArgs a) {
   constexpr int NE = E::VEC;
   constexpr int S = kWave / G;
   constexpr int NSTEPS = kWave / S;
-  constexpr int U = NSTEPS < 8 ? NSTEPS : 8;
+  constexpr int U = NSTEPS < 4 ? NSTEPS : 4;  // L2-hit gathers: 4 steps in flight, more waves
   const int lane = lane_id();
   const int sub = lane / G;
   const int gl = lane % G;
@@ -293,8 +293,13 @@ void spmm_sum_xcd_kernel(XcdArgs a) {
       const int kl = row_of(w.incl, std::min<int32_t>(v, w.total - 1));
       const int64_t e = v + shfl64(w.d, kl);
       const bool ok = v < w.total;
-      const int32_t cl = ok ? (int32_t)std::min<int64_t>(std::max<int64_t>(col[e], 0), a.rhs_rows - 1) : 0;
-      const float wl = ok ? E::load1(val, e) : 0.f;
+      const int32_t cl = ok ? (int32_t)std::min<int64_t>(std::max<int64_t>((int64_t)load_stream(col + e), 0), a.rhs_rows - 1) : 0;
+      // the edge weight, streamed past L2 (which holds the tile's rows)
+      float wl = 0.f;
+      if (ok) {
+        if constexpr (DT == OGN_F32) wl = __uint_as_float(load_stream(reinterpret_cast<const uint32_t*>(val) + e));
+        else wl = E::load1(val, e);
+      }
       for (int j0 = 0; j0 < nsteps; j0 += U) {
         uint4 xr[U];
         float wv[U];
