@@ -406,9 +406,14 @@ int ogn_gather_coo(const int64_t* index, const void* src, int64_t batch, int64_t
  * ogn_xcd_plan: builds the plan of (rowptr, col) into `plan`
  *   (ogn_xcd_plan_bytes bytes): row-aligned chunks of about 8192 edges and,
  *   for every row, where each of 8 column tiles (n_cols / 8 columns wide)
- *   starts in its edge range.  *sorted = 1 when every row's columns are
- *   sorted (only then do the tiles follow column ranges; the results are
- *   right either way).  Waits for a 4-byte read.  Fewer than 2^31 edges.
+ *   starts in its edge range.  *sorted (the plan state) = 0 when a row's
+ *   columns are not sorted (the tiles then do not follow column ranges; the
+ *   results are right either way), 1 when they are, 2 when they are and
+ *   n_cols <= 2^19, so that the plan also holds every column as a 16-bit
+ *   offset from its tile's first column (2 bytes per edge streamed instead
+ *   of the index).  Waits for a 4-byte read.  Fewer than 2^31 edges.
+ * The run functions take that state as plan_state (2: read the 16-bit
+ *   columns, which needs rhs_rows / n equal to the plan's n_cols; else col).
  * ogn_sddmm_dot_xcd: out[e] = dot(lhs[row(e)], rhs[col[e]]) (lhs_target =
  *   row, rhs_target = col), k * element size 64, 128, 256 or 512 bytes.
  * ogn_spmm_sum_xcd: out[r] = sum_e value[e] * mat[col[e]] (one weight per
@@ -419,11 +424,11 @@ int ogn_xcd_plan(const void* rowptr, const void* col, int index_dtype, int64_t m
                  void* plan, size_t plan_bytes, int* sorted, void* stream);
 int ogn_sddmm_dot_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, int index_dtype, const void* lhs,
                       int64_t lhs_rows, const void* rhs, int64_t rhs_rows, int64_t k, int dtype, void* out,
-                      void* stream);
+                      int plan_state, void* stream);
 size_t ogn_spmm_sum_xcd_workspace_size(int64_t m, int64_t k);
 int ogn_spmm_sum_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, int index_dtype, const void* value,
                      const void* mat, int64_t n, int64_t k, int dtype, void* out, int out_dtype, void* workspace,
-                     size_t workspace_bytes, void* stream);
+                     size_t workspace_bytes, int plan_state, void* stream);
 
 /* ------------------------------------------------------------------ measurement
  * Practical memory ceilings, reported by bench.py beside the 8 TB/s HBM

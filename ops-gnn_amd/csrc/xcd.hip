@@ -41,8 +41,13 @@ int64_t tile_width(int64_t n_cols) { return std::max<int64_t>(1, (n_cols + kTile
 struct XcdPlan {
   const int64_t* chunk_row;  // [nchunks + 1]
   const int64_t* split;      // [kTiles + 1][m]
+  const uint16_t* col16;     // [nnz]: column minus its tile's first column
   int64_t m, nchunks;
 };
+
+// Tile-relative 16-bit columns are kept when a tile spans at most 2^16
+// columns (n_cols <= 2^19) and the rows are sorted.
+constexpr int64_t kCol16MaxCols = (int64_t)kTiles << 16;
 
 // Plan memory: a 256-byte header (word 0: the build's unsorted-row flag),
 // chunk_row padded to 32 entries, then split.
@@ -53,6 +58,7 @@ XcdPlan plan_view(const void* plan, int64_t m, int64_t nnz) {
   p.nchunks = plan_chunks(nnz);
   p.chunk_row = static_cast<const int64_t*>(plan) + kHeaderWords;
   p.split = p.chunk_row + ((p.nchunks + 1 + 31) / 32 * 32);
+  p.col16 = reinterpret_cast<const uint16_t*>(p.split + (int64_t)(kTiles + 1) * m);
   p.m = m;
   return p;
 }
@@ -60,7 +66,8 @@ XcdPlan plan_view(const void* plan, int64_t m, int64_t nnz) {
 size_t plan_bytes(int64_t m, int64_t nnz) {
   const int64_t nc = plan_chunks(nnz);
   return sizeof(int64_t) *
-         ((size_t)kHeaderWords + (size_t)((nc + 1 + 31) / 32 * 32) + (size_t)(kTiles + 1) * (size_t)m);
+             ((size_t)kHeaderWords + (size_t)((nc + 1 + 31) / 32 * 32) + (size_t)(kTiles + 1) * (size_t)m) +
+         sizeof(uint16_t) * (size_t)((nnz + 127) / 128 * 128);
 }
 
 // ------------------------------------------------------------------ plan
@@ -117,6 +124,16 @@ __global__ __launch_bounds__(kBlock) void plan_sorted_kernel(const IDX* __restri
   if (__ballot(bad) && lane_id() == 0) atomicOr(unsorted, 1);
 }
 
+template <typename IDX>
+__global__ __launch_bounds__(kBlock) void plan_col16_kernel(const IDX* __restrict__ col, int64_t nnz, int64_t tile_w,
+                                                             uint16_t* __restrict__ col16) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= nnz) return;
+  const int64_t c = std::max<int64_t>((int64_t)col[e], 0);
+  const int64_t t = std::min<int64_t>(c / tile_w, kTiles - 1);
+  col16[e] = (uint16_t)std::min<int64_t>(c - t * tile_w, 65535);
+}
+
 __global__ void zero_int_kernel(int* p) { *p = 0; }
 
 // ------------------------------------------------------------------ shared walk
@@ -160,6 +177,7 @@ __device__ __forceinline__ int row_of(int32_t incl, int32_t v) {
 
 struct XcdArgs {
   XcdPlan pl;
+  int64_t tile_w;   // columns per tile (tile t starts at t * tile_w)
   const void* col;
   const void* lhs;
   const void* rhs;  // the gathered table (SDDMM rhs, SpMM mat)
@@ -171,7 +189,7 @@ struct XcdArgs {
 };
 
 // ------------------------------------------------------------------ SDDMM dot
-template <int DT, typename IDX, int G>
+template <int DT, typename IDX, int G, bool C16>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4)))
 void sddmm_dot_xcd_kernel(XcdArgs a) {
   using E = Elem<DT>;
@@ -189,6 +207,13 @@ void sddmm_dot_xcd_kernel(XcdArgs a) {
   if (c >= pl.nchunks) return;
   const int64_t R0 = pl.chunk_row[c], R1 = pl.chunk_row[c + 1];
   const IDX* __restrict__ col = static_cast<const IDX*>(a.col);
+  // edge e's column: from the plan's 16-bit tile-relative copy (2 bytes per
+  // edge streamed instead of 4 or 8), or from col
+  const int64_t tile0 = (int64_t)t * a.tile_w;
+  auto column = [&](int64_t e) -> int64_t {
+    if constexpr (C16) return tile0 + (int64_t)load_stream(a.pl.col16 + e);
+    else return (int64_t)load_stream(col + e);
+  };
   const char* __restrict__ lhs = static_cast<const char*>(a.lhs);
   const char* __restrict__ rhs = static_cast<const char*>(a.rhs);
   const uint32_t row_bytes = (uint32_t)(a.k * sizeof(S_t));
@@ -203,7 +228,7 @@ void sddmm_dot_xcd_kernel(XcdArgs a) {
       const int nw = std::min<int32_t>(kWave, w.total - vb);
       const int kl = row_of(w.incl, std::min<int32_t>(v, w.total - 1));
       const int64_t e = v + shfl64(w.d, kl);
-      const int32_t cl = v < w.total ? (int32_t)std::min<int64_t>(std::max<int64_t>((int64_t)load_stream(col + e), 0), a.rhs_rows - 1) : 0;
+      const int32_t cl = v < w.total ? (int32_t)std::min<int64_t>(std::max<int64_t>(column(e), 0), a.rhs_rows - 1) : 0;
       float mine = 0.f;
       for (int j0 = 0; j0 < NSTEPS; j0 += U) {
         uint4 xr[U];
@@ -234,7 +259,7 @@ void sddmm_dot_xcd_kernel(XcdArgs a) {
 }
 
 // ------------------------------------------------------------------ SpMM sum
-template <int DT, typename IDX, int G>
+template <int DT, typename IDX, int G, bool C16>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4)))
 void spmm_sum_xcd_kernel(XcdArgs a) {
   using E = Elem<DT>;
@@ -252,6 +277,13 @@ void spmm_sum_xcd_kernel(XcdArgs a) {
   if (c >= pl.nchunks) return;
   const int64_t R0 = pl.chunk_row[c], R1 = pl.chunk_row[c + 1];
   const IDX* __restrict__ col = static_cast<const IDX*>(a.col);
+  // edge e's column: from the plan's 16-bit tile-relative copy (2 bytes per
+  // edge streamed instead of 4 or 8), or from col
+  const int64_t tile0 = (int64_t)t * a.tile_w;
+  auto column = [&](int64_t e) -> int64_t {
+    if constexpr (C16) return tile0 + (int64_t)load_stream(a.pl.col16 + e);
+    else return (int64_t)load_stream(col + e);
+  };
   const S_t* __restrict__ val = static_cast<const S_t*>(a.val);
   const char* __restrict__ mat = static_cast<const char*>(a.rhs);
   float* __restrict__ part = a.partial + (size_t)t * (size_t)pl.m * (size_t)a.k;
@@ -293,7 +325,7 @@ void spmm_sum_xcd_kernel(XcdArgs a) {
       const int kl = row_of(w.incl, std::min<int32_t>(v, w.total - 1));
       const int64_t e = v + shfl64(w.d, kl);
       const bool ok = v < w.total;
-      const int32_t cl = ok ? (int32_t)std::min<int64_t>(std::max<int64_t>((int64_t)load_stream(col + e), 0), a.rhs_rows - 1) : 0;
+      const int32_t cl = ok ? (int32_t)std::min<int64_t>(std::max<int64_t>(column(e), 0), a.rhs_rows - 1) : 0;
       // the edge weight, streamed past L2 (which holds the tile's rows)
       float wl = 0.f;
       if (ok) {
@@ -354,24 +386,34 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const float* __restrict
   store_floats<4, true>(out, ODT, i, s);
 }
 
-template <int DT, typename IDX>
-void launch_dot(int g, dim3 grid, hipStream_t s, const XcdArgs& a) {
+template <int DT, typename IDX, bool C16>
+void launch_dot_c(int g, dim3 grid, hipStream_t s, const XcdArgs& a) {
   switch (g) {
-    case 4: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 4>), grid, dim3(kBlock), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 8>), grid, dim3(kBlock), 0, s, a); break;
-    case 16: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 16>), grid, dim3(kBlock), 0, s, a); break;
-    default: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 32>), grid, dim3(kBlock), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 4, C16>), grid, dim3(kBlock), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 8, C16>), grid, dim3(kBlock), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 16, C16>), grid, dim3(kBlock), 0, s, a); break;
+    default: hipLaunchKernelGGL((sddmm_dot_xcd_kernel<DT, IDX, 32, C16>), grid, dim3(kBlock), 0, s, a); break;
   }
 }
 
 template <int DT, typename IDX>
-void launch_sum(int g, dim3 grid, hipStream_t s, const XcdArgs& a) {
+void launch_dot(int g, bool c16, dim3 grid, hipStream_t s, const XcdArgs& a) {
+  c16 ? launch_dot_c<DT, IDX, true>(g, grid, s, a) : launch_dot_c<DT, IDX, false>(g, grid, s, a);
+}
+
+template <int DT, typename IDX, bool C16>
+void launch_sum_c(int g, dim3 grid, hipStream_t s, const XcdArgs& a) {
   switch (g) {
-    case 4: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 4>), grid, dim3(kBlock), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 8>), grid, dim3(kBlock), 0, s, a); break;
-    case 16: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 16>), grid, dim3(kBlock), 0, s, a); break;
-    default: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 32>), grid, dim3(kBlock), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 4, C16>), grid, dim3(kBlock), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 8, C16>), grid, dim3(kBlock), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 16, C16>), grid, dim3(kBlock), 0, s, a); break;
+    default: hipLaunchKernelGGL((spmm_sum_xcd_kernel<DT, IDX, 32, C16>), grid, dim3(kBlock), 0, s, a); break;
   }
+}
+
+template <int DT, typename IDX>
+void launch_sum(int g, bool c16, dim3 grid, hipStream_t s, const XcdArgs& a) {
+  c16 ? launch_sum_c<DT, IDX, true>(g, grid, s, a) : launch_sum_c<DT, IDX, false>(g, grid, s, a);
 }
 
 // Feature rows of 64, 128, 256 or 512 bytes (G = 4 .. 32 lanes of 16 bytes).
@@ -411,30 +453,38 @@ int ogn_xcd_plan(const void* rowptr, const void* col, int index_dtype, int64_t m
   const unsigned rbk = (unsigned)((m + kBlock - 1) / kBlock);
   const unsigned wb = (unsigned)((m + 3) / 4);
   const int64_t tw = tile_width(n_cols);
+  const unsigned eb = (unsigned)((nnz + kBlock - 1) / kBlock);
   if (index_dtype == OGN_I64) {
     const int64_t* p = static_cast<const int64_t*>(rowptr);
     const int64_t* c = static_cast<const int64_t*>(col);
     hipLaunchKernelGGL(plan_chunk_rows_kernel<int64_t>, dim3(cb), dim3(kBlock), 0, s, p, m, pl.nchunks, chunk_row);
     hipLaunchKernelGGL(plan_split_kernel<int64_t>, dim3(rbk), dim3(kBlock), 0, s, p, c, m, tw, split);
     hipLaunchKernelGGL(plan_sorted_kernel<int64_t>, dim3(wb), dim3(kBlock), 0, s, p, c, m, flag);
+    if (n_cols <= kCol16MaxCols)
+      hipLaunchKernelGGL(plan_col16_kernel<int64_t>, dim3(eb), dim3(kBlock), 0, s, c, nnz, tw,
+                         const_cast<uint16_t*>(pl.col16));
   } else {
     const int32_t* p = static_cast<const int32_t*>(rowptr);
     const int32_t* c = static_cast<const int32_t*>(col);
     hipLaunchKernelGGL(plan_chunk_rows_kernel<int32_t>, dim3(cb), dim3(kBlock), 0, s, p, m, pl.nchunks, chunk_row);
     hipLaunchKernelGGL(plan_split_kernel<int32_t>, dim3(rbk), dim3(kBlock), 0, s, p, c, m, tw, split);
     hipLaunchKernelGGL(plan_sorted_kernel<int32_t>, dim3(wb), dim3(kBlock), 0, s, p, c, m, flag);
+    if (n_cols <= kCol16MaxCols)
+      hipLaunchKernelGGL(plan_col16_kernel<int32_t>, dim3(eb), dim3(kBlock), 0, s, c, nnz, tw,
+                         const_cast<uint16_t*>(pl.col16));
   }
   int host = 1;
   if (hipMemcpyAsync(&host, flag, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
       hipStreamSynchronize(s) != hipSuccess)
     return fail(OGN_EHIP, "ogn_xcd_plan: reading the sortedness flag failed");
-  *sorted = host == 0 ? 1 : 0;
+  // 1: sorted rows; 2: sorted, and the 16-bit tile-relative columns are kept
+  *sorted = host != 0 ? 0 : (n_cols <= kCol16MaxCols ? 2 : 1);
   return check_launch("ogn_xcd_plan");
 }
 
 int ogn_sddmm_dot_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, int index_dtype, const void* lhs,
                       int64_t lhs_rows, const void* rhs, int64_t rhs_rows, int64_t k, int dtype, void* out,
-                      void* stream) {
+                      int plan_state, void* stream) {
   if (!plan || !col || !lhs || !rhs || !out) return fail(OGN_EINVAL, "ogn_sddmm_dot_xcd: null pointer");
   if (m <= 0 || nnz <= 0 || nnz >= (int64_t)1 << 31) return fail(OGN_EINVAL, "ogn_sddmm_dot_xcd: sizes");
   if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
@@ -447,6 +497,7 @@ int ogn_sddmm_dot_xcd(const void* plan, int64_t m, int64_t nnz, const void* col,
     return fail(OGN_EUNSUPPORTED, "ogn_sddmm_dot_xcd: feature tables above 4 GiB");
   XcdArgs a{};
   a.pl = plan_view(plan, m, nnz);
+  a.tile_w = tile_width(rhs_rows);
   a.col = col;
   a.lhs = lhs;
   a.rhs = rhs;
@@ -456,13 +507,16 @@ int ogn_sddmm_dot_xcd(const void* plan, int64_t m, int64_t nnz, const void* col,
   a.k = k;
   a.dt = dtype;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // plan_state: what ogn_xcd_plan reported; 2 = 16-bit columns kept (the
+  // plan was built with n_cols = rhs_rows)
+  const bool c16 = plan_state == 2;
   TimedLaunch tl("sddmm_xcd", s);
   const bool i64 = index_dtype == OGN_I64;
   const dim3 grid = xcd_grid(a.pl);
   switch (dtype) {
-    case OGN_F32: i64 ? launch_dot<OGN_F32, int64_t>(g, grid, s, a) : launch_dot<OGN_F32, int32_t>(g, grid, s, a); break;
-    case OGN_F16: i64 ? launch_dot<OGN_F16, int64_t>(g, grid, s, a) : launch_dot<OGN_F16, int32_t>(g, grid, s, a); break;
-    default: i64 ? launch_dot<OGN_BF16, int64_t>(g, grid, s, a) : launch_dot<OGN_BF16, int32_t>(g, grid, s, a); break;
+    case OGN_F32: i64 ? launch_dot<OGN_F32, int64_t>(g, c16, grid, s, a) : launch_dot<OGN_F32, int32_t>(g, c16, grid, s, a); break;
+    case OGN_F16: i64 ? launch_dot<OGN_F16, int64_t>(g, c16, grid, s, a) : launch_dot<OGN_F16, int32_t>(g, c16, grid, s, a); break;
+    default: i64 ? launch_dot<OGN_BF16, int64_t>(g, c16, grid, s, a) : launch_dot<OGN_BF16, int32_t>(g, c16, grid, s, a); break;
   }
   return check_launch("ogn_sddmm_dot_xcd");
 }
@@ -474,7 +528,7 @@ size_t ogn_spmm_sum_xcd_workspace_size(int64_t m, int64_t k) {
 
 int ogn_spmm_sum_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, int index_dtype, const void* value,
                      const void* mat, int64_t n, int64_t k, int dtype, void* out, int out_dtype, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     size_t workspace_bytes, int plan_state, void* stream) {
   if (!plan || !col || !value || !mat || !out) return fail(OGN_EINVAL, "ogn_spmm_sum_xcd: null pointer");
   if (m <= 0 || nnz <= 0 || nnz >= (int64_t)1 << 31) return fail(OGN_EINVAL, "ogn_spmm_sum_xcd: sizes");
   if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
@@ -490,6 +544,7 @@ int ogn_spmm_sum_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, 
     return fail(OGN_EINVAL, "ogn_spmm_sum_xcd: workspace too small or unaligned");
   XcdArgs a{};
   a.pl = plan_view(plan, m, nnz);
+  a.tile_w = tile_width(n);
   a.col = col;
   a.rhs = mat;
   a.val = value;
@@ -499,13 +554,14 @@ int ogn_spmm_sum_xcd(const void* plan, int64_t m, int64_t nnz, const void* col, 
   a.dt = dtype;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool i64 = index_dtype == OGN_I64;
+  const bool c16 = plan_state == 2;
   {
     TimedLaunch tl("spmm_xcd", s);
     const dim3 grid = xcd_grid(a.pl);
     switch (dtype) {
-      case OGN_F32: i64 ? launch_sum<OGN_F32, int64_t>(g, grid, s, a) : launch_sum<OGN_F32, int32_t>(g, grid, s, a); break;
-      case OGN_F16: i64 ? launch_sum<OGN_F16, int64_t>(g, grid, s, a) : launch_sum<OGN_F16, int32_t>(g, grid, s, a); break;
-      default: i64 ? launch_sum<OGN_BF16, int64_t>(g, grid, s, a) : launch_sum<OGN_BF16, int32_t>(g, grid, s, a); break;
+      case OGN_F32: i64 ? launch_sum<OGN_F32, int64_t>(g, c16, grid, s, a) : launch_sum<OGN_F32, int32_t>(g, c16, grid, s, a); break;
+      case OGN_F16: i64 ? launch_sum<OGN_F16, int64_t>(g, c16, grid, s, a) : launch_sum<OGN_F16, int32_t>(g, c16, grid, s, a); break;
+      default: i64 ? launch_sum<OGN_BF16, int64_t>(g, c16, grid, s, a) : launch_sum<OGN_BF16, int32_t>(g, c16, grid, s, a); break;
     }
   }
   {

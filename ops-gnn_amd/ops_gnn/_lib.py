@@ -88,9 +88,10 @@ SIGNATURES = {
     "ogn_calibrate_gather": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "ogn_xcd_plan_bytes": (_sz, [_i64, _i64]),
     "ogn_xcd_plan": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _sz, _vp, _vp]),
-    "ogn_sddmm_dot_xcd": (_int, [_vp, _i64, _i64, _vp, _int, _vp, _i64, _vp, _i64, _i64, _int, _vp, _vp]),
+    "ogn_sddmm_dot_xcd": (_int, [_vp, _i64, _i64, _vp, _int, _vp, _i64, _vp, _i64, _i64, _int, _vp, _int, _vp]),
     "ogn_spmm_sum_xcd_workspace_size": (_sz, [_i64, _i64]),
-    "ogn_spmm_sum_xcd": (_int, [_vp, _i64, _i64, _vp, _int, _vp, _vp, _i64, _i64, _int, _vp, _int, _vp, _sz, _vp]),
+    "ogn_spmm_sum_xcd": (_int, [_vp, _i64, _i64, _vp, _int, _vp, _vp, _i64, _i64, _int, _vp, _int, _vp, _sz, _int,
+                                 _vp]),
     "ogn_calibrate_stream": (_int, [_vp, _vp, _i64, _vp, _vp]),
 }
 

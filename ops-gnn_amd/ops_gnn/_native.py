@@ -126,10 +126,11 @@ def xcd_wanted(table_rows: int, row_bytes: int, nnz: int) -> bool:
     return XCD_TABLE_BYTES[0] <= table_rows * row_bytes <= XCD_TABLE_BYTES[1] and nnz >= XCD_MIN_EDGES
 
 
-def xcd_plan(ptr: torch.Tensor, col: torch.Tensor, n_cols: int) -> Optional[torch.Tensor]:
-    """The kept XCD plan of (ptr, col), or None when a row's columns are not
-    sorted (the tiles would not follow column ranges).  Cached per version of
-    col, together with ptr's address, version and n_cols."""
+def xcd_plan(ptr: torch.Tensor, col: torch.Tensor, n_cols: int):
+    """(plan, state) of the kept XCD plan of (ptr, col), or None when a row's
+    columns are not sorted (the tiles would not follow column ranges); state
+    2 means the plan also holds 16-bit tile-relative columns.  Cached per
+    version of col, together with ptr's address, version and n_cols."""
     import ctypes
 
     global _XCD_PLANS
@@ -144,10 +145,10 @@ def xcd_plan(ptr: torch.Tensor, col: torch.Tensor, n_cols: int) -> Optional[torc
         sorted_flag = ctypes.c_int(0)
         check(lib.ogn_xcd_plan(dptr(ptr), dptr(col), _index_code(ptr), m, n_cols, nnz, dptr(plan), plan.numel(),
                                ctypes.byref(sorted_flag), stream_of(col)), "xcd plan")
-        hit = (plan, sorted_flag.value == 1)
+        hit = (plan, sorted_flag.value)
         per_col.clear()
         per_col[info] = hit
-    return hit[0] if hit[1] else None
+    return hit if hit[1] > 0 else None
 
 
 def sddmm_dot_xcd(ptr, col, lhs, rhs, out) -> bool:
@@ -159,12 +160,12 @@ def sddmm_dot_xcd(ptr, col, lhs, rhs, out) -> bool:
         return False
     if lhs.data_ptr() % 16 or rhs.data_ptr() % 16 or ptr.dtype != col.dtype:
         return False
-    plan = xcd_plan(ptr, col, rhs.size(0))
-    if plan is None:
+    kept = xcd_plan(ptr, col, rhs.size(0))
+    if kept is None:
         return False
-    check(lib.ogn_sddmm_dot_xcd(dptr(plan), ptr.numel() - 1, nnz, dptr(col), _index_code(ptr), dptr(lhs),
+    check(lib.ogn_sddmm_dot_xcd(dptr(kept[0]), ptr.numel() - 1, nnz, dptr(col), _index_code(ptr), dptr(lhs),
                                 lhs.size(0), dptr(rhs), rhs.size(0), k, _lib.TORCH_TO_OGN[lhs.dtype], dptr(out),
-                                stream_of(lhs)), "sddmm_csr (xcd)")
+                                kept[1], stream_of(lhs)), "sddmm_csr (xcd)")
     return True
 
 
@@ -179,14 +180,14 @@ def spmm_sum_xcd(ptr, col, value, mat, out) -> bool:
         return False
     if not xcd_wanted(n, k * mat.element_size(), nnz) or mat.data_ptr() % 16 or out.data_ptr() % 16:
         return False
-    plan = xcd_plan(ptr, col, n)
-    if plan is None:
+    kept = xcd_plan(ptr, col, n)
+    if kept is None:
         return False
     ws_bytes = lib.ogn_spmm_sum_xcd_workspace_size(m, k)
     ws = _lib.workspace(ws_bytes, mat.device)
-    check(lib.ogn_spmm_sum_xcd(dptr(plan), m, nnz, dptr(col), _index_code(ptr), dptr(value), dptr(mat), n, k,
+    check(lib.ogn_spmm_sum_xcd(dptr(kept[0]), m, nnz, dptr(col), _index_code(ptr), dptr(value), dptr(mat), n, k,
                                _lib.TORCH_TO_OGN[mat.dtype], dptr(out), _lib.TORCH_TO_OGN[out.dtype], dptr(ws),
-                               ws_bytes, stream_of(mat)), "spmm (xcd)")
+                               ws_bytes, kept[1], stream_of(mat)), "spmm (xcd)")
     return True
 
 

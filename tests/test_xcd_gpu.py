@@ -156,7 +156,7 @@ def test_unsorted_columns_fall_back_and_direct_call_is_right(ogn, oracle, force_
     assert flag.value == 0
     out = torch.empty(col.numel(), dtype=torch.float16, device="cuda")
     _lib.check(L.ogn_sddmm_dot_xcd(_lib.dptr(plan), m, col.numel(), _lib.dptr(c), _lib.I64, _lib.dptr(q), m,
-                                   _lib.dptr(kk), n, k, _lib.TORCH_TO_OGN[torch.float16], _lib.dptr(out),
+                                   _lib.dptr(kk), n, k, _lib.TORCH_TO_OGN[torch.float16], _lib.dptr(out), 0,
                                    _lib.stream_of(q)), "sddmm xcd")
     assert np.array_equal(_bits(out), _bits(got)), "direct call on unsorted columns"
 
@@ -200,3 +200,29 @@ def test_size_selects_the_path(ogn, oracle):
     out = ogn.csr_spmm(p, c, val, kk, "sum")
     ref2 = _untiled(lambda: ogn.csr_spmm(p, c, val, kk, "sum"))
     np.testing.assert_allclose(out.float().cpu().numpy(), ref2.float().cpu().numpy(), rtol=1e-2, atol=1e-3)
+
+
+def test_wide_tables_read_the_index(ogn, oracle, force_xcd):
+    # more than 2^19 columns: tiles wider than 2^16 columns, so the plan keeps
+    # no 16-bit columns (state 1) and the kernels read col
+    from ops_gnn import _native
+
+    rng = np.random.default_rng(17)
+    m, n, k = 2000, 600_000, 16
+    deg = rng.poisson(50, m)
+    deg[3] = 12_000
+    col = np.concatenate([np.sort(rng.integers(0, n, d)) for d in deg]).astype(np.int64)
+    ptr = torch.from_numpy(np.concatenate([[0], np.cumsum(deg)]).astype(np.int64))
+    p, c = ptr.cuda(), torch.from_numpy(col).cuda()
+    kept = _native.xcd_plan(p, c, n)
+    assert kept is not None and kept[1] == 1
+    q = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).cuda()
+    kk = torch.from_numpy(rng.standard_normal((n, k)).astype(np.float32)).cuda()
+    got = ogn.sddmm_csr(p, c, q, kk, "dot")
+    ref = _untiled(lambda: ogn.sddmm_csr(p, c, q, kk, "dot"))
+    assert np.array_equal(_bits(got), _bits(ref)), "wide-table xcd sddmm"
+    val = torch.from_numpy(rng.random(col.size).astype(np.float32)).cuda()
+    out = ogn.csr_spmm(p, c, val, kk, "sum")
+    gold, _ = oracle.spmm_csr(ptr, torch.from_numpy(col), val.cpu(), kk.cpu(), "sum")
+    scale, _ = oracle.spmm_csr(ptr, torch.from_numpy(col), val.cpu().abs(), kk.cpu().abs(), "sum")
+    assert_sum_close(out, gold, scale, torch.float32, "wide-table xcd spmm")
