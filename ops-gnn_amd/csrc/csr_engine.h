@@ -287,11 +287,18 @@ __device__ __forceinline__ int64_t chunk_row_end(const Params& p, int64_t pb, in
   return std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c + 1], 0), p.m - 1);
 }
 
-// A chunk of short rows: on average at most S positions (one step) per row,
-// so that the step schedule would finish a row -- a cross-lane combine --
-// about every step.  Such chunks run short_chunk instead.
+// Chunks that run short_chunk instead of the step schedule: those where
+// some row both starts and ends (two or more row boundaries), or on average
+// at most S positions (one step) per row.  The step schedule finishes every
+// row with a cross-lane combine, which short_chunk spends only on rows long
+// enough to be folded by the whole wave; chunks with at most one row
+// boundary are the interior and the ends of long rows, where the step
+// schedule's long runs fold whole windows.  Config 5 scatter (Zipf degrees:
+// rows of 1-2 positions around hub rows) main kernel: sum / max / logsumexp
+// 1.28 / 1.53 / 1.46 ms with the mean rule alone, 1.24 / 1.41 / 1.28 ms.
+constexpr int64_t kWaveRowMin = 16;
 __device__ __forceinline__ bool chunk_is_short(int64_t r0, int64_t r_end, int64_t lo, int64_t hi, int S) {
-  return (r_end - r0) * S >= hi - lo;
+  return r_end - r0 >= 2 || (r_end - r0) * S >= hi - lo;
 }
 
 // Variants.  V_FIRST and V_LATER fix the common cases at compile time --
@@ -315,14 +322,17 @@ constexpr int engine_waves() {
   return DT != OGN_F32 && RK != RK_SUM ? 3 : 4;
 }
 
-// Chunks of short rows (contiguous mode, fast variants; see chunk_is_short),
-// run by engine_kernel's wave for chunk c instead of the step schedule: the
-// chunk's rows are dealt to the S sub-groups in turn, each sub-group folds
-// its row's positions (four loads in flight) on its own -- no cross-lane
-// combine -- and finishes the row, or leaves the same head / tail record as
-// the step schedule for a row that crosses the chunk's edge.  The extremum
-// direction is a template parameter, and argument positions are int32
-// offsets from the chunk start.
+// Chunks of many row boundaries (contiguous mode, fast variants; see
+// chunk_is_short), run by engine_kernel's wave for chunk c instead of the
+// step schedule: the chunk's rows are dealt to the S sub-groups in turn, each
+// sub-group folds its row's positions (four loads in flight) on its own --
+// no cross-lane combine -- and finishes the row, or leaves the same head /
+// tail record as the step schedule for a row that crosses the chunk's edge.
+// Rows with more positions in the chunk than L are skipped there and folded
+// afterwards by the whole wave, one at a time: sub-group s takes positions
+// s, s + S, ... (eight loads in flight) and the S partials are merged in
+// position order.  The extremum direction is a template parameter, and
+// argument positions are int32 offsets from the chunk start.
 template <int DT, int G, bool VL, int RK, int VAR, bool MIN>
 __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t lo, int64_t hi, int64_t r0,
                                             int64_t r_end) {
@@ -345,12 +355,12 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
   const S_t* __restrict__ srcb = static_cast<const S_t*>(p.src) + b * p.src_bstride;
   // rows r0 .. r_end - 1 end inside the chunk; r_end (< m) may start inside it
   const int64_t r_last = std::min<int64_t>(r_end, M - 1);
-  for (int64_t r = r0 + sub; r <= r_last; r += S) {
-    const int64_t rs = ptr[r], re = ptr[r + 1];
-    if (r == r_end && rs >= hi) break;  // starts in the next chunk
-    const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(std::min<int64_t>(re, hi), p.n);
-    float acc[NE], best[NE];
-    int32_t barg[NE];
+  // Rows with more than L positions inside the chunk (L: twice the chunk's
+  // mean row length, at least kWaveRowMin) are left to the whole wave
+  // (below), so that one long row does not hold up the sub-groups that fold
+  // the short rows dealt beside it.
+  const int64_t L = std::max<int64_t>(kWaveRowMin, 2 * (hi - lo) / std::max<int64_t>(1, r_last - r0 + 1));
+  auto init = [&](float* acc, float* best, int32_t* barg) {
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
       acc[i] = 0.f;
@@ -360,41 +370,26 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
                              : (VAR == V_LATER ? (MIN ? __builtin_inff() : -__builtin_inff()) : __builtin_nanf(""));
       barg[i] = kNone32;
     }
-    for (int64_t e0 = a; e0 < z; e0 += kU) {
-      float x[kU][NE];
+  };
+  auto fold = [&](const float* x, int32_t off, float* acc, float* best, int32_t* barg) {
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        // conditional: most of these rows hold 1-2 positions, and loading
-        // all four packets regardless was measured 15 % slower
-        const bool ok = e0 + u < z;
-        if constexpr (VL) {
-          E::unpack(ok ? load16(srcb + (e0 + u) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
-        } else {
-          x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + kc) : 0.f;
-        }
-      }
-      const int32_t off = (int32_t)(e0 - lo);
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        if (e0 + u >= z) break;
-#pragma unroll
-        for (int i = 0; i < NE; ++i) {
-          const float pv = x[u][i];
-          if constexpr (RK == RK_MINMAX) {
-            bool take;
-            if constexpr (VAR == V_LATER) take = MIN ? pv <= best[i] : pv >= best[i];
-            else take = !(MIN ? pv >= best[i] : pv <= best[i]) && pv == pv;
-            best[i] = take ? pv : best[i];
-            barg[i] = take ? off + u : barg[i];
-          } else if constexpr (RK == RK_LSE) {
-            lse_add(best[i], acc[i], pv);
-          } else {
-            acc[i] += pv;
-          }
-        }
+    for (int i = 0; i < NE; ++i) {
+      const float pv = x[i];
+      if constexpr (RK == RK_MINMAX) {
+        bool take;
+        if constexpr (VAR == V_LATER) take = MIN ? pv <= best[i] : pv >= best[i];
+        else take = !(MIN ? pv >= best[i] : pv <= best[i]) && pv == pv;
+        best[i] = take ? pv : best[i];
+        barg[i] = take ? off : barg[i];
+      } else if constexpr (RK == RK_LSE) {
+        lse_add(best[i], acc[i], pv);
+      } else {
+        acc[i] += pv;
       }
     }
-    if (!kok) continue;
+  };
+  // Write row r's result (whole row in the chunk) or its head / tail record.
+  auto emit = [&](int64_t r, int64_t rs, int64_t re, const float* acc, const float* best, const int32_t* barg) {
     if (re > hi || rs < lo) {
       // partial row: tail if it goes on past the chunk, else head (it began before)
       const bool head = re <= hi;
@@ -425,6 +420,121 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
           for (int i = 0; i < NE; ++i) p.arg[off + i] = ag[i];
         }
       }
+    }
+  };
+  for (int64_t r = r0 + sub; r <= r_last; r += S) {
+    const int64_t rs = ptr[r], re = ptr[r + 1];
+    if (r == r_end && rs >= hi) break;  // starts in the next chunk
+    const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(std::min<int64_t>(re, hi), p.n);
+    if (z - a > L) continue;  // the wave's
+    float acc[NE], best[NE];
+    int32_t barg[NE];
+    init(acc, best, barg);
+    for (int64_t e0 = a; e0 < z; e0 += kU) {
+      float x[kU][NE];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        // conditional: most of these rows hold 1-2 positions, and loading
+        // all four packets regardless was measured 15 % slower
+        const bool ok = e0 + u < z;
+        if constexpr (VL) {
+          E::unpack(ok ? load16(srcb + (e0 + u) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+        } else {
+          x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + kc) : 0.f;
+        }
+      }
+      const int32_t off = (int32_t)(e0 - lo);
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        if (e0 + u >= z) break;
+        fold(x[u], off + u, acc, best, barg);
+      }
+    }
+    if (!kok) continue;
+    emit(r, rs, re, acc, best, barg);
+  }
+  // Long rows: sub-group s folds positions a + s, a + s + S, ... (kW steps
+  // in flight), then the sub-group partials are merged in position order.
+  constexpr int kW = 8;
+  for (int64_t w = r0; w <= r_last; w += kWave) {
+    bool lg = false;
+    if (w + lane <= r_last) {
+      const int64_t rr = w + lane;
+      const int64_t rs = ptr[rr], re = ptr[rr + 1];
+      const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(std::min<int64_t>(re, hi), p.n);
+      lg = !(rr == r_end && rs >= hi) && z - a > L;
+    }
+    uint64_t mask = __ballot(lg);
+    while (mask) {
+      const int j = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const int64_t r = w + j;
+      const int64_t rs = ptr[r], re = ptr[r + 1];
+      const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(std::min<int64_t>(re, hi), p.n);
+      float acc[NE], best[NE];
+      int32_t barg[NE];
+      init(acc, best, barg);
+      int64_t e0 = a;
+      for (; e0 + kW * S <= z; e0 += kW * S) {
+        float x[kW][NE];
+#pragma unroll
+        for (int u = 0; u < kW; ++u) {
+          if constexpr (VL) E::unpack(load16(srcb + (e0 + sub + u * S) * K + kc), x[u]);
+          else x[u][0] = E::load1(srcb, (e0 + sub + u * S) * K + kc);
+        }
+#pragma unroll
+        for (int u = 0; u < kW; ++u) fold(x[u], (int32_t)(e0 + sub + u * S - lo), acc, best, barg);
+      }
+      {
+        float x[kW][NE];
+#pragma unroll
+        for (int u = 0; u < kW; ++u) {
+          const bool ok = e0 + sub + u * S < z;
+          if constexpr (VL) {
+            E::unpack(ok ? load16(srcb + (e0 + sub + u * S) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+          } else {
+            x[u][0] = ok ? E::load1(srcb, (e0 + sub + u * S) * K + kc) : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kW; ++u)
+          if (e0 + sub + u * S < z) fold(x[u], (int32_t)(e0 + sub + u * S - lo), acc, best, barg);
+      }
+      // butterfly over sub-groups; lower sub-groups hold earlier positions
+      auto round = [&](auto offc) {
+        constexpr int off = decltype(offc)::value;
+        const bool upper = (lane & off) != 0;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+          if constexpr (RK == RK_MINMAX) {
+            const float ob = xor_shfl<off>(best[i]);
+            const int32_t oa = xor_shfl<off>(barg[i]);
+            const bool tie = VAR == V_LATER ? oa > barg[i] : oa < barg[i];
+            const bool take = oa != kNone32 && (barg[i] == kNone32 || (MIN ? ob < best[i] : ob > best[i]) ||
+                                                (ob == best[i] && tie));
+            best[i] = take ? ob : best[i];
+            barg[i] = take ? oa : barg[i];
+          } else if constexpr (RK == RK_LSE) {
+            const float om = xor_shfl<off>(best[i]);
+            const float os = xor_shfl<off>(acc[i]);
+            float m1 = upper ? om : best[i], s1 = upper ? os : acc[i];
+            const float m2 = upper ? best[i] : om, s2 = upper ? acc[i] : os;
+            lse_merge(m1, s1, m2, s2);
+            best[i] = m1;
+            acc[i] = s1;
+          } else {
+            const float o = xor_shfl<off>(acc[i]);
+            acc[i] = upper ? o + acc[i] : acc[i] + o;
+          }
+        }
+      };
+      if constexpr (G <= 1) round(std::integral_constant<int, 1>{});
+      if constexpr (G <= 2) round(std::integral_constant<int, 2>{});
+      if constexpr (G <= 4) round(std::integral_constant<int, 4>{});
+      if constexpr (G <= 8) round(std::integral_constant<int, 8>{});
+      if constexpr (G <= 16) round(std::integral_constant<int, 16>{});
+      if constexpr (G <= 32) round(std::integral_constant<int, 32>{});
+      if (sub == 0 && kok) emit(r, rs, re, acc, best, barg);
     }
   }
 }

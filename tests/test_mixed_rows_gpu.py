@@ -1,0 +1,121 @@
+"""GPU parity for engine chunks that mix short rows with long ones.
+
+A contiguous-mode chunk holding two or more row boundaries has its rows
+dealt to the wave's sub-groups, one row each, except rows with more than
+L positions in the chunk (twice the chunk's mean row length, at least 16),
+which the whole wave folds afterwards with a position-ordered merge of the
+sub-group partials.  These inputs put long rows (17 .. 3000 positions)
+between runs of 0-3 position rows, at forced small chunks (64 and 256
+positions: long rows then also cross chunk edges, leaving head / tail
+records from the wave fold) and at the default chunk size.  Same bars as
+the other parity tests: min/max values and args bit-exact, sums within
+rel 1e-5 (fp32) / 1e-2 (fp16, bf16) of the oracle.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_exact, assert_sum_close, cast_like
+
+pytestmark = pytest.mark.gpu
+
+
+def _lengths(seed, rows=4000):
+    rng = np.random.default_rng(seed)
+    kind = rng.random(rows)
+    lengths = np.where(kind < 0.2, 0, rng.integers(1, 4, rows))
+    mid = kind > 0.9
+    lengths[mid] = rng.integers(4, 40, int(mid.sum()))
+    long_ = kind > 0.98
+    lengths[long_] = rng.integers(17, 3000, int(long_.sum()))
+    lengths[5] = 5000  # one long row near the start
+    return lengths.astype(np.int64)
+
+
+@pytest.fixture(params=[64, 256, None], ids=["chunk64", "chunk256", "default"])
+def chunk(request):
+    old = os.environ.get("OGN_ENGINE_CHUNK")
+    if request.param is not None:
+        os.environ["OGN_ENGINE_CHUNK"] = str(request.param)
+    yield request.param
+    if old is None:
+        os.environ.pop("OGN_ENGINE_CHUNK", None)
+    else:
+        os.environ["OGN_ENGINE_CHUNK"] = old
+
+
+def _src(rng, n, feat, dtype, ties):
+    if ties:
+        a = rng.integers(-4, 5, size=(n, feat)).astype(np.float32)
+    else:
+        a = rng.standard_normal((n, feat)).astype(np.float32)
+    return torch.from_numpy(a).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("feat", [1, 4, 32, 33, 128])
+def test_segment_csr_mixed_rows(ogn, oracle, chunk, dtype, reduce, feat):
+    lengths = _lengths(feat)
+    rng = np.random.default_rng(100 + feat)
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)]))
+    src = _src(rng, int(lengths.sum()), feat, dtype, reduce in ("min", "max"))
+    res = getattr(ogn, f"segment_{reduce}_csr")(src.cuda(), indptr.cuda())
+    out, arg = res if isinstance(res, tuple) else (res, None)
+    gold, garg = oracle.segment_csr(src, indptr, reduce)
+    what = f"mixed/{chunk}/{dtype}/{reduce}/f{feat}"
+    if arg is not None:
+        assert_exact(out, cast_like(gold, dtype), what + " values")
+        assert_exact(arg, garg, what + " arg")
+    else:
+        scale, _ = oracle.segment_csr(src.float().abs(), indptr, reduce)
+        assert_sum_close(out, gold, scale, dtype, what)
+
+
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("feat", [1, 32])
+def test_scatter_and_coo_mixed_rows(ogn, oracle, chunk, reduce, feat):
+    # later-tie rule (scatter / segment_coo) and out seeds through the wave fold
+    lengths = _lengths(7 + feat)
+    rng = np.random.default_rng(3 + feat)
+    m = lengths.size
+    index = np.repeat(np.arange(m), lengths)
+    src = _src(rng, index.size, feat, torch.float32, True)
+    out = torch.from_numpy(rng.integers(-4, 5, size=(m, feat)).astype(np.float32))
+    res = getattr(ogn, f"segment_{reduce}_coo")(src.cuda(), torch.from_numpy(index).cuda(), out.clone().cuda(), m)
+    got, arg = res if isinstance(res, tuple) else (res, None)
+    gold, garg = oracle.segment_coo(src, index, m, reduce, out.double().numpy())
+    if arg is not None:
+        assert_exact(got, gold, "coo values")
+        assert_exact(arg, garg, "coo arg")
+    else:
+        scale, _ = oracle.segment_coo(src.abs(), index, m, reduce, out.double().abs().numpy())
+        assert_sum_close(got, gold, scale, torch.float32, "coo")
+    res = ogn.scatter(src.cuda(), torch.from_numpy(index).cuda(), 0, dim_size=m, reduce=reduce)
+    got = res[0] if isinstance(res, tuple) else res
+    gold, _ = oracle.scatter(src.numpy(), index[:, None], 0, m, reduce)
+    if reduce in ("min", "max"):
+        assert_exact(got, gold, "scatter")
+    else:
+        scale, _ = oracle.scatter(np.abs(src.numpy()), index[:, None], 0, m, reduce)
+        assert_sum_close(got, gold, scale, torch.float32, "scatter")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("feat", [1, 32, 33])
+def test_segment_logsumexp_mixed_rows(ogn, oracle, chunk, dtype, feat):
+    lengths = _lengths(11)
+    rng = np.random.default_rng(11)
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)]))
+    src = torch.from_numpy((rng.standard_normal((int(lengths.sum()), feat)) * 4).astype(np.float32)).to(dtype)
+    long_rows = np.nonzero(lengths > 100)[0]
+    r0, r1 = int(long_rows[0]), int(long_rows[-1])
+    src[int(indptr[r0]) + 40, 0] = float("inf")  # inside a long row: +inf
+    src[int(indptr[r1]) + 70, -1] = float("nan")  # inside another: NaN
+    got = ogn.segment_logsumexp(src.cuda(), indptr.cuda()).float().cpu().numpy()
+    gold = cast_like(oracle.segment_logsumexp(src, indptr), dtype)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    np.testing.assert_allclose(got, gold, rtol=tol, atol=tol)
