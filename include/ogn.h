@@ -209,8 +209,12 @@ int ogn_ptr2ind(const void* ptr, int index_dtype, int64_t rows, int64_t numel, i
  * follows each operator's rule (segment_csr: narrow(sum) / narrow(count)
  * truncating, 0 for a zero narrowed count; segment_coo: the same with the
  * exact mean for a zero narrowed count; scatter: floor division by the count,
- * narrowed and clamped to >= 1 for 8/16-bit types).  Exact dtypes need no
- * workspace and support sum, mean, min, max (and prod for scatter).
+ * narrowed and clamped to >= 1 for 8/16-bit types).  Exact dtypes support
+ * sum, mean, min, max (and prod for scatter).  For the integer dtypes the
+ * workspace holds partial results of segments longer than 4096 rows, folded
+ * in parallel pieces; with a smaller workspace (or none) such segments are
+ * folded by one thread per feature packet, with the same result.  float64
+ * needs no workspace (its sums keep the serial order).
  * reduce: sum, mean, min, max, prod, lse.  arg (int64, optional, min/max
  * only) gets positions along the reduction dim.
  *
@@ -245,7 +249,8 @@ enum { OGN_SEM_SEGMENT_CSR = 0, OGN_SEM_SEGMENT_COO = 1, OGN_SEM_SCATTER = 2, OG
  *  OGN_SEG_HAS_OUT -- out holds seeds (see semantics above).
  *  OGN_SEG_SHORT_SEGMENTS -- the caller knows that no segment holds more
  *    than 4096 rows; the pass that pre-folds the partial results of segments
- *    spanning many wavefront chunks is then not launched.
+ *    spanning many wavefront chunks (integer dtypes: the piece pass) is then
+ *    not launched.
  *  OGN_SEG_KEEP_LAYOUT -- the caller keeps `workspace` for later calls with
  *    the same indptr (same address, same contents) on the same stream; the
  *    library records which pointer array and chunk plan the workspace's

@@ -852,7 +852,8 @@ extern "C" {
 
 size_t ogn_segment_reduce_workspace_size(int64_t batch, int64_t length, int64_t segments, int64_t k,
                                          int64_t ptr_batches, int in_dtype, int reduce) {
-  if (batch <= 0 || length < 0 || segments < 0 || k <= 0 || is_exact_dtype(in_dtype)) return 0;
+  if (batch <= 0 || length < 0 || segments < 0 || k <= 0) return 0;
+  if (is_exact_dtype(in_dtype)) return exact_segment_workspace_size(batch, length, k, in_dtype, reduce);
   const int rk = rk_of(reduce);
   const Plan pa = make_plan(length, k, in_dtype, true);
   const Plan pu = make_plan(length, k, in_dtype, false);
@@ -882,7 +883,8 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
   const bool has_out = (flags & OGN_SEG_HAS_OUT) != 0;
   if (exact)
     return exact_segment_reduce(indptr, ptr_batches, src, dtype, batch, length, segments, k, out, arg, reduce,
-                                semantics, has_out ? 1 : 0, static_cast<hipStream_t>(stream));
+                                semantics, has_out ? 1 : 0, (flags & OGN_SEG_SHORT_SEGMENTS) != 0, workspace,
+                                workspace_bytes, static_cast<hipStream_t>(stream));
 
   const bool aligned = is_aligned(src, 16) && is_aligned(out, 16);
   const Plan pl = make_plan(length, k, dtype, aligned);

@@ -9,10 +9,16 @@ namespace ogn {
 // int8, uint8, int16, int32, int64, float64
 bool is_exact_dtype(int dt);
 
-// Arguments as ogn_segment_reduce (validated by the caller; no workspace).
+// Workspace for the piece records of long integer segments (0: none used).
+size_t exact_segment_workspace_size(int64_t batch, int64_t length, int64_t k, int dtype, int reduce);
+
+// Arguments as ogn_segment_reduce (validated by the caller).  A workspace
+// smaller than exact_segment_workspace_size, or the short-segments hint,
+// folds every segment serially.
 int exact_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* src, int dtype, int64_t batch,
                          int64_t length, int64_t segments, int64_t k, void* out, int64_t* arg, int reduce,
-                         int semantics, int has_out, hipStream_t stream);
+                         int semantics, int has_out, bool short_segments, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 
 size_t exact_scatter_workspace_size(int64_t cells, int reduce);
 

@@ -9,7 +9,14 @@
 // Contiguous segments (segment_csr, segment_coo, sorted-index scatter): one
 // thread per (batch, segment, 16-byte feature packet) folds the segment's
 // rows in order -- deterministic, one writer per output, loads of one row
-// coalesced across the threads of a segment.  Unsorted scatter: 64-bit
+// coalesced across the threads of a segment.  Integer segments longer than
+// kLongSeg rows are first cut into fixed pieces of kPieceRows positions,
+// folded in parallel (piece_kernel) into partial records, and the segment's
+// thread then folds its records in position order: ring sums and products
+// do not depend on the grouping, and extremum records carry their position
+// and follow the same tie rule, so results are those of the serial fold
+// while a hub segment no longer serialises on one thread.  float64 keeps
+// the serial fold (its sum depends on the order).  Unsorted scatter: 64-bit
 // atomics into a workspace (integer add/min/max are associative, so the
 // result does not depend on the order; float64 sum/prod does, as in any
 // atomic scatter), a second pass for the "later writer wins" arg, and a
@@ -106,18 +113,106 @@ struct alignas(sizeof(T) * V) Pack {
 // ------------------------------------------------------------------ contiguous segments
 enum { RC_SUM = 0, RC_PROD = 1, RC_MINMAX = 2 };
 
+// Segments of more rows than kLongSeg take the piece records; a piece is
+// kPieceRows positions (so a long segment spans at least three pieces).
+constexpr int64_t kLongSeg = 4096;
+constexpr int64_t kPieceRows = 2048;
+
 struct SegArgs {
+  // piece records, or null: value rec[((b * npieces + piece) * 2 + w) * k + f]
+  // (w = 0: the segment holding the piece's first position, w = 1: the one
+  // holding its last position, when that is another segment) and, for
+  // min / max, the extremum's position at the same index of recpos
+  int64_t* rec;
+  int64_t* recpos;
+  int64_t npieces;
   const int64_t* ptr;
   int64_t ptr_bstride;
   const void* src;
   void* out;
   int64_t* arg;
-  int64_t length, segs, k;
+  int64_t length, segs, k, batch;
   int64_t total;    // batch * segs * packets
   FastDiv packets;  // packets per row (k / V)
   FastDiv segs_d;
   int sem, has_out, mean, is_max;
 };
+
+// Index of the segment holding position x (ptr[s] <= x < ptr[s + 1]), or -1.
+__device__ __forceinline__ int64_t segment_of(const int64_t* ptr, int64_t segs, int64_t x) {
+  int64_t lo = 0, hi = segs + 1;  // first index with ptr[i] > x
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ptr[mid] <= x) lo = mid + 1;
+    else hi = mid;
+  }
+  const int64_t s = lo - 1;
+  return s >= 0 && s < segs && x < ptr[s + 1] ? s : -1;
+}
+
+// One thread per (batch, piece, packet): the partial records of the (at most
+// two) long segments overlapping the piece.
+template <int DT, int V, int RC>
+__global__ __launch_bounds__(256) void piece_kernel(SegArgs a) {
+  using T = typename Store<DT>::T;
+  using A = Acc<DT>;
+  const int64_t packets = a.k / V;
+  const int64_t total = a.batch * a.npieces * packets;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t c = i % packets;
+    const int64_t t = i / packets;
+    const int64_t pc = t % a.npieces;
+    const int64_t b = t / a.npieces;
+    const int64_t* ptr = a.ptr + b * a.ptr_bstride;
+    const int64_t lo = pc * kPieceRows, hi = std::min<int64_t>(lo + kPieceRows, a.length);
+    const Pack<T, V>* src = reinterpret_cast<const Pack<T, V>*>(static_cast<const T*>(a.src) + (b * a.length) * a.k + c * V);
+    const int64_t row_step = a.k / V;
+    const int64_t s1 = segment_of(ptr, a.segs, lo);
+    const int64_t s2 = hi > lo ? segment_of(ptr, a.segs, hi - 1) : -1;
+#pragma unroll 1
+    for (int w = 0; w < 2; ++w) {
+      const int64_t s = w == 0 ? s1 : (s2 != s1 ? s2 : -1);
+      if (s < 0) continue;
+      const int64_t beg = ptr[s], end = ptr[s + 1];
+      if (end - beg <= kLongSeg) continue;
+      const int64_t from = std::max(beg, lo), to = std::min(end, hi);
+      A acc[V];
+      int64_t best[V];
+      {
+        const Pack<T, V> x = src[from * row_step];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          acc[j] = (A)x.v[j];
+          best[j] = from;
+        }
+      }
+      const bool strict = a.sem == OGN_SEM_SEGMENT_CSR;
+#pragma unroll 4
+      for (int64_t r = from + 1; r < to; ++r) {
+        const Pack<T, V> x = src[r * row_step];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const A xv = (A)x.v[j];
+          if constexpr (RC == RC_SUM) acc[j] = wadd(acc[j], xv);
+          if constexpr (RC == RC_PROD) acc[j] = wmul(acc[j], xv);
+          if constexpr (RC == RC_MINMAX) {
+            if (takes<DT>(xv, acc[j], a.is_max, strict)) {
+              acc[j] = xv;
+              best[j] = r;
+            }
+          }
+        }
+      }
+      const int64_t o = ((b * a.npieces + pc) * 2 + w) * a.k + c * V;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        a.rec[o + j] = (int64_t)acc[j];
+        if constexpr (RC == RC_MINMAX) a.recpos[o + j] = best[j];
+      }
+    }
+  }
+}
 
 template <int DT, int V, int RC>
 __global__ __launch_bounds__(256) void seg_kernel(SegArgs a) {
@@ -148,33 +243,75 @@ __global__ __launch_bounds__(256) void seg_kernel(SegArgs a) {
       if constexpr (RC == RC_PROD) acc[j] = seeded ? (A)seed.v[j] : (A)1;
       if constexpr (RC == RC_MINMAX) acc[j] = seeded ? (A)seed.v[j] : limit_of<DT>(a.is_max);
     }
-    int64_t r0 = beg;
-    bool strict = false;
-    if constexpr (RC == RC_MINMAX) {
-      // segment_csr / unseeded segment_coo start from the segment's first row
-      if (!seeded && a.sem != OGN_SEM_SCATTER && rows > 0) {
-        const Pack<T, V> x = src[beg * row_step];
+    if (a.rec && rows > kLongSeg) {
+      // fold the piece records in position order: the first piece's record
+      // 0 when the segment starts on the piece boundary, else its record 1;
+      // record 0 of every later piece
+      const int64_t pb = beg / kPieceRows, pe = (end - 1) / kPieceRows;
+      const int w0 = beg % kPieceRows != 0 ? 1 : 0;
+      auto rec_at = [&](int64_t pc, int w) { return ((b * a.npieces + pc) * 2 + w) * a.k + c * V; };
+      int64_t pc = pb;
+      bool strict = false;
+      if constexpr (RC == RC_MINMAX) {
+        // segment_csr / unseeded segment_coo start from the first record
+        // (taken here, not through a loop-carried "first" flag: with one,
+        // the gfx950 code kept later takes' positions but not their values)
+        if (!seeded && a.sem != OGN_SEM_SCATTER) {
+          const int64_t ro = rec_at(pb, w0);
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            acc[j] = (A)a.rec[ro + j];
+            best[j] = a.recpos[ro + j];
+          }
+          pc = pb + 1;
+        }
+        strict = a.sem == OGN_SEM_SEGMENT_CSR;
+      }
+#pragma unroll 4
+      for (; pc <= pe; ++pc) {
+        const int64_t ro = rec_at(pc, pc == pb ? w0 : 0);
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-          acc[j] = (A)x.v[j];
-          best[j] = beg;
+          const A xv = (A)a.rec[ro + j];
+          if constexpr (RC == RC_SUM) acc[j] = wadd(acc[j], xv);
+          if constexpr (RC == RC_PROD) acc[j] = wmul(acc[j], xv);
+          if constexpr (RC == RC_MINMAX) {
+            const int64_t xp = a.recpos[ro + j];  // loaded unconditionally: the loads pipeline
+            const bool tk = takes<DT>(xv, acc[j], a.is_max, strict);
+            acc[j] = tk ? xv : acc[j];
+            best[j] = tk ? xp : best[j];
+          }
         }
-        r0 = beg + 1;
       }
-      strict = a.sem == OGN_SEM_SEGMENT_CSR;
-    }
-#pragma unroll 4
-    for (int64_t r = r0; r < end; ++r) {
-      const Pack<T, V> x = src[r * row_step];
+    } else {
+      int64_t r0 = beg;
+      bool strict = false;
+      if constexpr (RC == RC_MINMAX) {
+        // segment_csr / unseeded segment_coo start from the segment's first row
+        if (!seeded && a.sem != OGN_SEM_SCATTER && rows > 0) {
+          const Pack<T, V> x = src[beg * row_step];
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const A xv = (A)x.v[j];
-        if constexpr (RC == RC_SUM) acc[j] = wadd(acc[j], xv);
-        if constexpr (RC == RC_PROD) acc[j] = wmul(acc[j], xv);
-        if constexpr (RC == RC_MINMAX) {
-          if (takes<DT>(xv, acc[j], a.is_max, strict)) {
-            acc[j] = xv;
-            best[j] = r;
+          for (int j = 0; j < V; ++j) {
+            acc[j] = (A)x.v[j];
+            best[j] = beg;
+          }
+          r0 = beg + 1;
+        }
+        strict = a.sem == OGN_SEM_SEGMENT_CSR;
+      }
+#pragma unroll 4
+      for (int64_t r = r0; r < end; ++r) {
+        const Pack<T, V> x = src[r * row_step];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const A xv = (A)x.v[j];
+          if constexpr (RC == RC_SUM) acc[j] = wadd(acc[j], xv);
+          if constexpr (RC == RC_PROD) acc[j] = wmul(acc[j], xv);
+          if constexpr (RC == RC_MINMAX) {
+            if (takes<DT>(xv, acc[j], a.is_max, strict)) {
+              acc[j] = xv;
+              best[j] = r;
+            }
           }
         }
       }
@@ -202,6 +339,16 @@ unsigned grid_for(int64_t total) {
 
 template <int DT, int V>
 void launch_seg(const SegArgs& a, int rc, hipStream_t s) {
+  if constexpr (DT != OGN_F64) {
+    if (a.rec) {
+      TimedLaunch t("segment_exact_pieces", s);
+      const dim3 g(grid_for(a.batch * a.npieces * (a.k / V)));
+      if (rc == RC_SUM) hipLaunchKernelGGL((piece_kernel<DT, V, RC_SUM>), g, dim3(256), 0, s, a);
+      else if (rc == RC_PROD) hipLaunchKernelGGL((piece_kernel<DT, V, RC_PROD>), g, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((piece_kernel<DT, V, RC_MINMAX>), g, dim3(256), 0, s, a);
+    }
+  }
+  TimedLaunch t("segment_exact", s);
   const dim3 grid(grid_for(a.total));
   if (rc == RC_SUM) hipLaunchKernelGGL((seg_kernel<DT, V, RC_SUM>), grid, dim3(256), 0, s, a);
   else if (rc == RC_PROD) hipLaunchKernelGGL((seg_kernel<DT, V, RC_PROD>), grid, dim3(256), 0, s, a);
@@ -377,9 +524,17 @@ bool is_exact_dtype(int dt) {
   return dt == OGN_I8 || dt == OGN_U8 || dt == OGN_I16 || dt == OGN_I32 || dt == OGN_I64 || dt == OGN_F64;
 }
 
+size_t exact_segment_workspace_size(int64_t batch, int64_t length, int64_t k, int dtype, int reduce) {
+  if (dtype == OGN_F64 || batch <= 0 || length <= kLongSeg || k <= 0) return 0;
+  const int64_t npieces = (length + kPieceRows - 1) / kPieceRows;
+  const size_t one = ((size_t)batch * npieces * 2 * k * sizeof(int64_t) + 255) / 256 * 256;
+  return (reduce == OGN_REDUCE_MIN || reduce == OGN_REDUCE_MAX) ? 2 * one : one;
+}
+
 int exact_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* src, int dtype, int64_t batch,
                          int64_t length, int64_t segments, int64_t k, void* out, int64_t* arg, int reduce,
-                         int semantics, int has_out, hipStream_t stream) {
+                         int semantics, int has_out, bool short_segments, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
   if (reduce == OGN_REDUCE_LSE || semantics == OGN_SEM_DGL)
     return fail(OGN_EUNSUPPORTED, "ogn_segment_reduce: logsumexp and DGL reductions need a floating dtype");
   if (reduce == OGN_REDUCE_PROD && semantics != OGN_SEM_SCATTER)
@@ -405,7 +560,16 @@ int exact_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void*
   a.mean = reduce == OGN_REDUCE_MEAN;
   a.is_max = reduce == OGN_REDUCE_MAX;
   const int rc = reduce == OGN_REDUCE_PROD ? RC_PROD : (reduce == OGN_REDUCE_MIN || reduce == OGN_REDUCE_MAX) ? RC_MINMAX : RC_SUM;
-  TimedLaunch t("segment_exact", stream);
+  a.batch = batch;
+  // long segments: piece records, when the caller's workspace holds them
+  // (without it, or with the short-segments hint, every segment is folded
+  // serially, with the same result)
+  const size_t need = exact_segment_workspace_size(batch, length, k, dtype, reduce);
+  if (need > 0 && !short_segments && workspace && workspace_bytes >= need) {
+    a.npieces = (length + kPieceRows - 1) / kPieceRows;
+    a.rec = static_cast<int64_t*>(workspace);
+    a.recpos = rc == RC_MINMAX ? reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + need / 2) : nullptr;
+  }
   switch (dtype) {
     case OGN_I8: launch_seg_dt<OGN_I8>(a, v, rc, stream); break;
     case OGN_U8: launch_seg_dt<OGN_U8>(a, v, rc, stream); break;

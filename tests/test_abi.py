@@ -55,3 +55,20 @@ def test_workspace_query_is_pure_host():
     a = L.lib.ogn_spmm_csr_workspace_size(100, 1000, 128, 1, L.F32, 0)
     b = L.lib.ogn_spmm_csr_workspace_size(100, 1000, 128, 1, L.F32, 3)
     assert 0 < a < b
+
+
+def test_exact_segment_workspace_sizes():
+    # integer dtypes: piece records (one int64 per feature and record, two
+    # records per 2048-position piece; min/max also keep positions), only
+    # when a segment can be longer than 4096 rows; float64: none
+    import ops_gnn._lib as L
+
+    i32 = L.TORCH_TO_OGN[__import__("torch").int32]
+    f64 = L.TORCH_TO_OGN[__import__("torch").float64]
+    size = L.lib.ogn_segment_reduce_workspace_size
+    assert size(1, 4096, 10, 8, 1, i32, L.R_SUM) == 0
+    s = size(1, 10_000, 10, 8, 1, i32, L.R_SUM)
+    assert s >= 5 * 2 * 8 * 8  # 5 pieces
+    assert size(1, 10_000, 10, 8, 1, i32, L.R_MAX) == 2 * s
+    assert size(2, 10_000, 10, 8, 2, i32, L.R_SUM) >= 2 * 5 * 2 * 8 * 8
+    assert size(1, 10_000, 10, 8, 1, f64, L.R_SUM) == 0
