@@ -1,10 +1,11 @@
 """DGL-style generalised CSR aggregation: spmm / bspmm.
 
-Mirror of the reference python/ops_gnn/spmm.py:292-321 and bspmm.py:17-28:
-the same call options (op, reduce, out, rhs), operand rules (copy_rhs may take
-its edge features through ``x``), rank alignment, error messages and
-reduction semantics (sum / mean / max / min; max and min propagate NaN; empty
-rows give 0).  Every case runs on HIP kernels:
+Drop-in for the reference's python/ops_gnn/spmm.py:292-321 and
+bspmm.py:17-28 call contract: the same call options (op, reduce, out, rhs),
+operand rules (copy_rhs may take its edge features through ``x``), rank
+alignment, error messages and reduction semantics (sum / mean / max / min;
+max and min propagate NaN; empty rows give 0).  Every case runs on HIP
+kernels:
   copy_lhs and the binary messages (mul / add / sub / div with an edge
   operand) -> the CSR engine in gather mode (ogn_spmm_csr_ex, DGL semantics);
   copy_rhs -> the contiguous-segment engine over the edge rows.
@@ -16,8 +17,7 @@ max / min.
 """
 
 import math
-from dataclasses import dataclass
-from typing import Optional, Tuple
+from typing import NamedTuple, Optional, Tuple
 
 import torch
 
@@ -30,38 +30,90 @@ _MSG = {"mul": _lib.MSG_MUL, "add": _lib.MSG_ADD, "sub": _lib.MSG_SUB, "div": _l
         "copy_lhs": _lib.MSG_MUL}
 _FEATURE_DTYPES = (torch.float16, torch.float32, torch.bfloat16)
 
+# Call options after (indptr, indices, x), in positional order, with defaults.
+_OPTIONS = (("op", "copy_lhs"), ("reduce", "sum"), ("out", None), ("rhs", None))
 
-@dataclass(frozen=True)
-class _SpmmRequest:
+
+class _Call(NamedTuple):
+    """One spmm / bspmm call: the CSR pattern and the message / reduction
+    (the feature operands travel separately, as autograd inputs)."""
+    api: str  # "spmm" or "bspmm"
     indptr: torch.Tensor
     indices: torch.Tensor
-    x: Optional[torch.Tensor]
     op: str
     reduce: str
-    out: Optional[torch.Tensor]
-    rhs: Optional[torch.Tensor]
-    batched: bool
+
+    @property
+    def batched(self) -> bool:
+        return self.api == "bspmm"
 
 
-def _normalize_operands(x, rhs, op):
+def _bind_options(api: str, args: tuple, kwargs: dict) -> dict:
+    """The call options from the extra positional and keyword arguments,
+    refused as Python refuses a bad call of a function with this signature."""
+    names = [name for name, _ in _OPTIONS]
+    if len(args) > len(names):
+        raise TypeError(f"{api} accepts at most seven positional arguments")
+    given = dict(zip(names, args))
+    twice = [name for name in given if name in kwargs]
+    if twice:
+        raise TypeError(f"{api} got multiple values for argument '{twice[0]}'")
+    unknown = sorted(set(kwargs).difference(names))
+    if unknown:
+        raise TypeError(f"{api} got an unexpected keyword argument '{unknown[0]}'")
+    return {**dict(_OPTIONS), **given, **kwargs}
+
+
+def _operands(op: str, x, rhs):
+    """(node, edge): the operand gathered per edge through `indices`, and the
+    one holding a row per edge.  copy_rhs takes its edge rows from whichever
+    of x / rhs was given."""
+    if op == "copy_rhs":
+        supplied = [t for t in (rhs, x) if t is not None]
+        if len(supplied) > 1:
+            raise ValueError("copy_rhs accepts edge features through either x or rhs, not both")
+        if not supplied:
+            raise ValueError("copy_rhs requires edge features")
+        return None, supplied[0]
     if op == "copy_lhs":
         if x is None or rhs is not None:
             raise ValueError("copy_lhs requires x and does not accept rhs")
         return x, None
-    if op == "copy_rhs":
-        if rhs is not None:
-            if x is not None:
-                raise ValueError("copy_rhs accepts edge features through either x or rhs, not both")
-            return None, rhs
-        if x is None:
-            raise ValueError("copy_rhs requires edge features")
-        return None, x
     if x is None or rhs is None:
         raise ValueError(f"{op} requires both x and rhs")
     return x, rhs
 
 
-def _validate(request: _SpmmRequest, lhs, rhs):
+def _check_arguments(api: str, tensors: dict, op, reduce) -> None:
+    """Argument kinds and option values, before any operand is looked at."""
+    for name, value in tensors.items():
+        if value is not None and not isinstance(value, torch.Tensor):
+            raise TypeError(f"{api}: {name} must be a Tensor")
+    if not (isinstance(op, str) and op in _MESSAGE_OPS):
+        raise RuntimeError(f"{api}: op must be copy_lhs, copy_rhs, add, sub, mul or div")
+    if not (isinstance(reduce, str) and reduce in _REDUCE_OPS):
+        raise RuntimeError(f"{api}: reduce must be sum, max, min or mean")
+
+
+def _deliver(result: torch.Tensor, out: Optional[torch.Tensor], grad_required: bool) -> torch.Tensor:
+    """The result, or `out` holding it (refused under autograd, or when it
+    does not match the result exactly)."""
+    if out is None:
+        return result
+    refusals = (
+        (lambda: grad_required, "out is not supported when feature tensors require gradients"),
+        (lambda: (out.shape, out.dtype, out.device) != (result.shape, result.dtype, result.device),
+         "out must match the result shape, dtype and device"),
+        (lambda: not out.is_contiguous() or out.requires_grad,
+         "out must be contiguous and must not require gradients"),
+    )
+    for refused, message in refusals:
+        if refused():
+            raise RuntimeError(message)
+    return out.copy_(result)
+
+
+def _validate(request: _Call, lhs, rhs):
     features = [v for v in (lhs, rhs) if v is not None]
     for name, value in (("indptr", request.indptr), ("indices", request.indices)):
         if not isinstance(value, torch.Tensor):
@@ -124,7 +176,7 @@ def _align(lhs, rhs):
     return pad(lhs), pad(rhs)
 
 
-def _forward(request: _SpmmRequest, lhs, rhs, want_arg: bool = False):
+def _forward(request: _Call, lhs, rhs, want_arg: bool = False):
     """(out, arg): out [rows, *feat]; arg [rows, k] int64 (the edge each
     max / min element came from, E for an empty row; the first NaN edge for
     a NaN result; the first extremal edge among ties) when `want_arg`."""
@@ -170,7 +222,7 @@ def _forward(request: _SpmmRequest, lhs, rhs, want_arg: bool = False):
     return out.reshape((rows,) + feat), arg
 
 
-def _message_shapes(request: _SpmmRequest, x, w):
+def _message_shapes(request: _Call, x, w):
     """(feat, aligned x shape, aligned w shape) of the forward's messages."""
     if request.op == "copy_rhs":
         return tuple(w.shape[1:]), None, tuple(w.shape)
@@ -294,60 +346,24 @@ class _DglSpmm(torch.autograd.Function):
         return gx, gw_out, None
 
 
-def _spmm(request: _SpmmRequest) -> torch.Tensor:
-    api = "bspmm" if request.batched else "spmm"
-    for name, value in (("indptr", request.indptr), ("indices", request.indices), ("x", request.x),
-                        ("rhs", request.rhs), ("out", request.out)):
-        if value is not None and not isinstance(value, torch.Tensor):
-            raise TypeError(f"{api}: {name} must be a Tensor")
-    if not isinstance(request.op, str) or request.op not in _MESSAGE_OPS:
-        raise RuntimeError(f"{api}: op must be copy_lhs, copy_rhs, add, sub, mul or div")
-    if not isinstance(request.reduce, str) or request.reduce not in _REDUCE_OPS:
-        raise RuntimeError(f"{api}: reduce must be sum, max, min or mean")
-    lhs, edge = _normalize_operands(request.x, request.rhs, request.op)
-    _validate(request, lhs, edge)
-    grad_required = torch.is_grad_enabled() and any(v is not None and v.requires_grad for v in (lhs, edge))
-    if grad_required:
-        result = _DglSpmm.apply(lhs, edge, request)
-    else:
-        result = _forward(request, lhs, edge)[0]
-    out = request.out
-    if out is None:
-        return result
-    if grad_required:
-        raise RuntimeError("out is not supported when feature tensors require gradients")
-    if out.shape != result.shape or out.dtype != result.dtype or out.device != result.device:
-        raise RuntimeError("out must match the result shape, dtype and device")
-    if not out.is_contiguous() or out.requires_grad:
-        raise RuntimeError("out must be contiguous and must not require gradients")
-    out.copy_(result)
-    return out
-
-
-def _parse_call_options(api: str, args: tuple, kwargs: dict) -> Tuple:
-    names = ("op", "reduce", "out", "rhs")
-    if len(args) > len(names):
-        raise TypeError(f"{api} accepts at most seven positional arguments")
-    options = {"op": "copy_lhs", "reduce": "sum", "out": None, "rhs": None}
-    for name, value in zip(names, args):
-        if name in kwargs:
-            raise TypeError(f"{api} got multiple values for argument '{name}'")
-        options[name] = value
-    unexpected = set(kwargs) - set(names)
-    if unexpected:
-        raise TypeError(f"{api} got an unexpected keyword argument '{sorted(unexpected)[0]}'")
-    options.update(kwargs)
-    return options["op"], options["reduce"], options["out"], options["rhs"]
+def _aggregate(api: str, indptr, indices, x, args: tuple, kwargs: dict) -> torch.Tensor:
+    options = _bind_options(api, args, kwargs)
+    op, reduce, out, rhs = options["op"], options["reduce"], options["out"], options["rhs"]
+    _check_arguments(api, {"indptr": indptr, "indices": indices, "x": x, "rhs": rhs, "out": out}, op, reduce)
+    node, edge = _operands(op, x, rhs)
+    call = _Call(api, indptr, indices, op, reduce)
+    _validate(call, node, edge)
+    grad_required = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (node, edge))
+    result = _DglSpmm.apply(node, edge, call) if grad_required else _forward(call, node, edge)[0]
+    return _deliver(result, out, grad_required)
 
 
 def spmm(indptr: torch.Tensor, indices: torch.Tensor, x: Optional[torch.Tensor] = None, *args, **kwargs):
     """Generalised CSR aggregation: out[r] = reduce_{e in row r} msg(x[indices[e]], rhs[e])."""
-    op, reduce, out, rhs = _parse_call_options("spmm", args, kwargs)
-    return _spmm(_SpmmRequest(indptr, indices, x, op, reduce, out, rhs, False))
+    return _aggregate("spmm", indptr, indices, x, args, kwargs)
 
 
 def bspmm(indptr: torch.Tensor, indices: torch.Tensor, x: Optional[torch.Tensor] = None, *args, **kwargs):
     """Batched form of :func:`spmm`: at least one feature tensor has rank >= 3;
     trailing feature dims broadcast after the item axis."""
-    op, reduce, out, rhs = _parse_call_options("bspmm", args, kwargs)
-    return _spmm(_SpmmRequest(indptr, indices, x, op, reduce, out, rhs, True))
+    return _aggregate("bspmm", indptr, indices, x, args, kwargs)
