@@ -285,6 +285,20 @@ int ogn_ind2ptr_batched(const int64_t* ind, int64_t batches, int64_t numel, int6
  * scatter (python/ops_gnn/scatter.py:134-178). */
 int ogn_index_facts(const int64_t* ind, int64_t numel, int64_t* facts, void* stream);
 
+/* Stable sort of n int64 keys known to lie in [0, max_key] (max_key below
+ * 2^32, n below 2^31): perm[i] = position of the i-th smallest key, equal keys
+ * in position order; sorted_keys (optional, may be NULL) = the keys in that
+ * order.  The COO -> CSR and CSR -> CSC permutation step (reference
+ * python/ops_gnn/torch_sparse_spmm.py:273-342, argsort(stable) there; the
+ * values are then permuted by a row gather, ogn_gather_coo).  Radix sort over the
+ * ceil(log2(max_key + 1)) low key bits with 32-bit keys and positions; the
+ * workspace (ogn_sort_rows_workspace_size: 0 when the sizes are out of range
+ * or no GPU answers the query) holds them and the sort's temporary storage.
+ * Not capturable in a HIP graph. */
+size_t ogn_sort_rows_workspace_size(int64_t n, int64_t max_key);
+int ogn_sort_rows(const int64_t* keys, int64_t n, int64_t max_key, int64_t* sorted_keys, int64_t* perm,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
 /* Log-sum-exp statistics of sorted groups (contiguous segments, shared
  * indptr [segments + 1]): m_out[b, g, f] = max (unclamped; -inf for an empty
  * group) and s_out[b, g, f] = sum(exp(x - clamp(max, +-FLT_MAX))), both fp32.

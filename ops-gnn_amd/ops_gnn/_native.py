@@ -326,6 +326,26 @@ def index_probe(index: torch.Tensor) -> Tuple[bool, int, int]:
     return (unsorted != 0, mn, mx)
 
 
+def sort_rows(keys: torch.Tensor, max_key: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(sorted keys, perm) of a 1-D int64 key tensor with every key in
+    [0, max_key]: a stable sort (equal keys keep their order), as
+    torch.sort(keys, stable=True).  Sizes beyond the native sort's range
+    (2^31 keys, keys of 2^32 or more) take torch.sort on the device."""
+    n = keys.numel()
+    keys = keys.contiguous()
+    ws_bytes = lib.ogn_sort_rows_workspace_size(n, max_key) if n > 0 else 0
+    if n > 0 and ws_bytes == 0:
+        return torch.sort(keys, stable=True)
+    sorted_keys = torch.empty_like(keys)
+    perm = torch.empty(n, dtype=torch.int64, device=keys.device)
+    if n == 0:
+        return sorted_keys, perm
+    ws = _lib.workspace(ws_bytes, keys.device)
+    check(lib.ogn_sort_rows(dptr(keys), n, max_key, dptr(sorted_keys), dptr(perm), dptr(ws), ws_bytes,
+                            stream_of(keys)), "sort_rows")
+    return sorted_keys, perm
+
+
 def index_facts(index: torch.Tensor, key: Optional[torch.Tensor] = None) -> Tuple[bool, int, int]:
     """(sorted, min, max) of an int32 / int64 index (index_probe), cached per
     tensor version of `key` (default: `index` itself; pass the caller's

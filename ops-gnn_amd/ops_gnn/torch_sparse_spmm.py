@@ -257,7 +257,8 @@ class _Csr:
         row = self.row if self.row is not None else _C.convert(self.ptr, e, False)
         perm = self.perm
         if perm is None:
-            sorted_col, perm = torch.sort(self.col, stable=True)
+            # columns lie in [0, n) (validated with the CSR): bounded-key sort
+            sorted_col, perm = _native.sort_rows(self.col, max(self.n - 1, 0))
         else:
             sorted_col = self.col[perm]
         colptr = self.colptr if self.colptr is not None else _C.convert(sorted_col, self.n + 1, True)
@@ -414,7 +415,7 @@ def _coo_layout_uncached(index: torch.Tensor, m: int):
         raise ValueError("COO row out of range")
     if not unsorted:
         return _C.convert(row, m + 1, True), index[1].clone(), None
-    sorted_row, perm = torch.sort(row, stable=True)
+    sorted_row, perm = _native.sort_rows(row, m - 1)
     return _C.convert(sorted_row, m + 1, True), index[1][perm], perm
 
 

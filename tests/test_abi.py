@@ -72,3 +72,14 @@ def test_exact_segment_workspace_sizes():
     assert size(1, 10_000, 10, 8, 1, i32, L.R_MAX) == 2 * s
     assert size(2, 10_000, 10, 8, 2, i32, L.R_SUM) >= 2 * 5 * 2 * 8 * 8
     assert size(1, 10_000, 10, 8, 1, f64, L.R_SUM) == 0
+
+
+def test_sort_rows_refuses_out_of_range_sizes_without_gpu():
+    # checked before any device work
+    import ops_gnn._lib as L
+
+    assert L.lib.ogn_sort_rows(None, 2**31, 10, None, None, None, 0, None) == 2  # OGN_EUNSUPPORTED
+    assert L.lib.ogn_sort_rows(None, 10, 2**32, None, None, None, 0, None) == 2
+    assert L.lib.ogn_sort_rows(None, -1, 10, None, None, None, 0, None) == 1  # OGN_EINVAL
+    assert L.lib.ogn_sort_rows(None, 0, 10, None, None, None, 0, None) == 0  # nothing to sort
+    assert L.lib.ogn_sort_rows_workspace_size(2**31, 10) == 0
