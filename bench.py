@@ -188,7 +188,7 @@ def main():
     ap.add_argument("--torch-compare", action="store_true",
                     help="also time torch's embedding_bag(sum, per_sample_weights) on the same CSR "
                          "(a library implementation of the same weighted row gather)")
-    ap.add_argument("--workload", choices=["spmm", "segment", "gat", "coo"], default="spmm",
+    ap.add_argument("--workload", choices=["spmm", "segment", "gat", "coo", "convert"], default="spmm",
                     help="spmm = config 3 (the headline metric); segment / gat / coo = configs 2 / 4 / 5")
     args = ap.parse_args()
 
@@ -199,7 +199,8 @@ def main():
         sys.exit(2)
 
     if args.workload != "spmm":
-        line = {"segment": bench_segment, "gat": bench_gat, "coo": bench_coo}[args.workload](args)
+        line = {"segment": bench_segment, "gat": bench_gat, "coo": bench_coo,
+                "convert": bench_convert}[args.workload](args)
         if args.copy_calibration:
             copy_calibration()
 
@@ -546,6 +547,65 @@ def bench_gat(args):
                  {"nodes": n, "nnz": e, "k": f}, ops, sddmm_kernel, comp["sddmm"], km[sddmm_kernel], cpu,
                  basis="compulsory: col + scores + Q and K read once (the per-edge K-row gathers hit the "
                        "256 MB MALL, since K is 29.8 MB)")
+
+
+def bench_convert(args):
+    """COO -> CSR of config 3's graph (2.45 M rows, 62 M edges, fp32 values)
+    given in a random edge order, through the torch_sparse frontend's
+    coo_to_csr: the stable sort by row (ogn_sort_rows), the row pointers and
+    the column and value permutation."""
+    import numpy as np
+    import torch
+
+    from ops_gnn import torch_sparse_spmm as tss
+    from ops_gnn.convert import ptr2ind_tensor
+    from ops_gnn.synthetic import cfg3_powerlaw_spmm
+
+    dev = torch.device("cuda:0")
+
+    def gpu_sort(keys):
+        t = torch.from_numpy(keys).to(dev)
+        return torch.sort(t).values.cpu().numpy()
+
+    ptr_np, col_np, val_np, _ = cfg3_powerlaw_spmm(sort_keys=gpu_sort, with_mat=False)
+    m, e = ptr_np.shape[0] - 1, int(ptr_np[-1])
+    ptr = torch.from_numpy(ptr_np).to(dev)
+    row = ptr2ind_tensor(ptr, e)
+    order = torch.randperm(e, device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    index = torch.stack([row[order], torch.from_numpy(col_np).to(dev)[order]]).contiguous()
+    value = torch.from_numpy(val_np).to(dev)[order].contiguous()
+    del row, order
+    # index and values in (20 B / edge), pointers, columns and values out
+    # (8 B / row + 12 B / edge), the permutation kept for the layout cache (8 B / edge)
+    nbytes = 40 * e + 8 * (m + 1)
+    sort_bytes = 16 * e  # the radix sort proper: 32-bit keys and positions, in and out
+    fn = lambda: tss.coo_to_csr(index, value, m)
+    with torch.no_grad():
+        ms = _timed(fn, args.steps, args.warmup)
+        kms = _kernel_ms(fn, args.steps, ["sort_rows_pack", "sort_rows_radix", "sort_rows_unpack"])
+    log(f"bench convert: {ms:.4f} ms, {nbytes / ms / 1e6:.1f} GB/s; sort kernels {kms}")
+    ops = {"coo_to_csr": {"ms": round(ms, 4), "GB/s": round(nbytes / ms / 1e6, 1), "bytes": nbytes},
+           "sort_rows": {k: round(v, 4) for k, v in kms.items()}}
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle
+
+        idx_np = index.cpu().numpy()
+        val_h = value.cpu().numpy()
+
+        def convert(r):
+            perm = np.argsort(idx_np[0, :r], kind="stable")
+            oracle.ind2ptr(idx_np[0, :r][perm], m)
+            return idx_np[1, :r][perm], val_h[:r][perm]
+
+        gbs, r, dt = _cpu_sample(convert, e, lambda r: 40 * r + 8 * (m + 1))
+        cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"numpy stable argsort + oracle_ind2ptr (C) + permutation on the first {r} edges "
+                         f"of the same COO input, {dt:.2f} s"}
+    return _line("COO -> CSR conversion effective GB/s (config 3 graph, random edge order)",
+                 nbytes / ms / 1e6, "GB/s", ms, args, "int64", "configs[2] graph: coo_to_csr",
+                 {"rows": m, "edges": e}, ops, "sort_rows_radix", sort_bytes, kms["sort_rows_radix"], cpu,
+                 basis="32-bit keys and positions in and out of the radix sort")
 
 
 def bench_coo(args):

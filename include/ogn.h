@@ -288,15 +288,20 @@ int ogn_index_facts(const int64_t* ind, int64_t numel, int64_t* facts, void* str
 /* Stable sort of n int64 keys known to lie in [0, max_key] (max_key below
  * 2^32, n below 2^31): perm[i] = position of the i-th smallest key, equal keys
  * in position order; sorted_keys (optional, may be NULL) = the keys in that
- * order.  The COO -> CSR and CSR -> CSC permutation step (reference
- * python/ops_gnn/torch_sparse_spmm.py:273-342, argsort(stable) there; the
- * values are then permuted by a row gather, ogn_gather_coo).  Radix sort over the
- * ceil(log2(max_key + 1)) low key bits with 32-bit keys and positions; the
- * workspace (ogn_sort_rows_workspace_size: 0 when the sizes are out of range
- * or no GPU answers the query) holds them and the sort's temporary storage.
- * Not capturable in a HIP graph. */
-size_t ogn_sort_rows_workspace_size(int64_t n, int64_t max_key);
+ * order; up to two companion arrays a, b (elements of a_bytes / b_bytes = 4
+ * or 8 bytes; 0 = none; b only with a) permuted alike: a_out[i] =
+ * a[perm[i]].  The COO -> CSR and CSR -> CSC permutation step (reference
+ * python/ops_gnn/torch_sparse_spmm.py:273-342: a stable argsort, then the
+ * columns and values indexed by it).  Radix sort over the
+ * ceil(log2(max_key + 1)) low key bits with 32-bit keys; the companions
+ * travel with the positions through the sort's passes.  The workspace
+ * (ogn_sort_rows_workspace_size with the same sizes and companion widths: 0
+ * when they are out of range or no GPU answers the query) holds the keys,
+ * the records and the sort's temporary storage.  Not capturable in a HIP
+ * graph. */
+size_t ogn_sort_rows_workspace_size(int64_t n, int64_t max_key, int a_bytes, int b_bytes);
 int ogn_sort_rows(const int64_t* keys, int64_t n, int64_t max_key, int64_t* sorted_keys, int64_t* perm,
+                  const void* a, void* a_out, int a_bytes, const void* b, void* b_out, int b_bytes,
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* Log-sum-exp statistics of sorted groups (contiguous segments, shared

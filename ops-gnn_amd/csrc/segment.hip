@@ -43,24 +43,66 @@ __global__ void facts_init_kernel(int64_t* facts) {
   facts[2] = INT64_MIN;
 }
 
+// Each thread reads 16-byte pairs (ind[j], ind[j + 1]) at 4 pairs in flight,
+// plus the element after each pair for the order test across pairs; j
+// starts at `first` (0, or 1 when ind is only 8-byte aligned), and thread 0
+// also takes the elements outside the pairs.  One atomic per block.
 __global__ __launch_bounds__(256) void index_facts_kernel(const int64_t* __restrict__ ind, int64_t numel,
-                                                          int64_t* facts) {
+                                                          int64_t first, int64_t* facts) {
   int64_t unsorted = 0, mn = INT64_MAX, mx = INT64_MIN;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < numel; i += stride) {
-    const int64_t v = ind[i];
+  auto take = [&](int64_t v) {
     mn = v < mn ? v : mn;
     mx = v > mx ? v : mx;
-    if (i + 1 < numel && ind[i + 1] < v) unsorted = 1;
+  };
+  const int64_t npairs = (numel - first) / 2;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int kU = 4;
+  for (int64_t p0 = t0; p0 < npairs; p0 += kU * stride) {
+    longlong2 v[kU];
+    int64_t nx[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t p = p0 + u * stride;
+      const int64_t j = first + 2 * p;
+      v[u] = p < npairs ? *reinterpret_cast<const longlong2*>(ind + j) : make_longlong2(INT64_MAX, INT64_MAX);
+      nx[u] = p < npairs && j + 2 < numel ? ind[j + 2] : INT64_MAX;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (p0 + u * stride >= npairs) break;
+      take(v[u].x);
+      take(v[u].y);
+      unsorted |= (v[u].x > v[u].y) | (v[u].y > nx[u]);
+    }
   }
-  // wave-level reduction, then one atomic per wave
+  if (t0 == 0) {
+    if (first == 1) {  // ind[0], before the first pair
+      take(ind[0]);
+      if (numel > 1 && ind[0] > ind[1]) unsorted = 1;
+    }
+    if ((numel - first) % 2 == 1) take(ind[numel - 1]);  // after the last pair (its order tested there)
+  }
   for (int off = 32; off > 0; off >>= 1) {
     unsorted |= __shfl_xor(unsorted, off);
     const int64_t omn = __shfl_xor(mn, off), omx = __shfl_xor(mx, off);
     mn = omn < mn ? omn : mn;
     mx = omx > mx ? omx : mx;
   }
+  __shared__ int64_t red[3][4];
+  const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
+    red[0][w] = unsorted;
+    red[1][w] = mn;
+    red[2][w] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) {
+      unsorted |= red[0][i];
+      mn = red[1][i] < mn ? red[1][i] : mn;
+      mx = red[2][i] > mx ? red[2][i] : mx;
+    }
     if (unsorted) atomicMax((unsigned long long*)&facts[0], 1ull);
     atomicMin((long long*)&facts[1], (long long)mn);
     atomicMax((long long*)&facts[2], (long long)mx);
@@ -1062,8 +1104,9 @@ int ogn_index_facts(const int64_t* ind, int64_t numel, int64_t* facts, void* str
   TimedLaunch t("index_facts", s);
   hipLaunchKernelGGL(facts_init_kernel, dim3(1), dim3(1), 0, s, facts);
   if (numel > 0) {
-    const int blocks = (int)std::min<int64_t>((numel + 255) / 256, 2048);
-    hipLaunchKernelGGL(index_facts_kernel, dim3(blocks), dim3(256), 0, s, ind, numel, facts);
+    const int64_t first = (reinterpret_cast<uintptr_t>(ind) & 15) ? 1 : 0;
+    const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>((numel / 2 + 255) / 256, 2048));
+    hipLaunchKernelGGL(index_facts_kernel, dim3(blocks), dim3(256), 0, s, ind, numel, first, facts);
   }
   return check_launch("ogn_index_facts");
 }

@@ -71,8 +71,8 @@ SIGNATURES = {
                                   _vp, _sz, _vp]),
     "ogn_ind2ptr_batched": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "ogn_index_facts": (_int, [_vp, _i64, _vp, _vp]),
-    "ogn_sort_rows_workspace_size": (_sz, [_i64, _i64]),
-    "ogn_sort_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "ogn_sort_rows_workspace_size": (_sz, [_i64, _i64, _int, _int]),
+    "ogn_sort_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _sz, _vp]),
     "ogn_segment_group_stats": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "ogn_segment_group_softmax_workspace_size": (_sz, [_i64, _i64, _i64, _int]),
     "ogn_segment_group_softmax": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _int, _int, _vp, _sz, _vp]),

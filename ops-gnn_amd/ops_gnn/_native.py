@@ -326,24 +326,42 @@ def index_probe(index: torch.Tensor) -> Tuple[bool, int, int]:
     return (unsorted != 0, mn, mx)
 
 
-def sort_rows(keys: torch.Tensor, max_key: int) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(sorted keys, perm) of a 1-D int64 key tensor with every key in
-    [0, max_key]: a stable sort (equal keys keep their order), as
-    torch.sort(keys, stable=True).  Sizes beyond the native sort's range
-    (2^31 keys, keys of 2^32 or more) take torch.sort on the device."""
+def sort_rows(keys: torch.Tensor, max_key: int, companions: Tuple[torch.Tensor, ...] = ()
+              ) -> Tuple[torch.Tensor, torch.Tensor, list]:
+    """(sorted keys, perm, permuted companions) of a 1-D int64 key tensor
+    with every key in [0, max_key]: a stable sort (equal keys keep their
+    order), as torch.sort(keys, stable=True), and each companion c (one
+    entry per key along dim 0) returned as c[perm].  Companions of 4- or
+    8-byte 1-D elements (at most two) are permuted inside the sort's last
+    pass; others by indexing.  Sizes beyond the native sort's range (2^31
+    keys, keys of 2^32 or more) take torch.sort on the device."""
     n = keys.numel()
     keys = keys.contiguous()
-    ws_bytes = lib.ogn_sort_rows_workspace_size(n, max_key) if n > 0 else 0
+    fused, outs = [], [None] * len(companions)
+    for i, c in enumerate(companions):
+        if len(fused) < 2 and c.dim() == 1 and c.element_size() in (4, 8) and c.device == keys.device:
+            outs[i] = torch.empty_like(c, memory_format=torch.contiguous_format)
+            fused.append((c.contiguous(), outs[i]))
+    widths = [src.element_size() for src, _ in fused] + [0] * (2 - len(fused))
+    ws_bytes = lib.ogn_sort_rows_workspace_size(n, max_key, *widths) if n > 0 else 0
     if n > 0 and ws_bytes == 0:
-        return torch.sort(keys, stable=True)
+        sk, perm = torch.sort(keys, stable=True)
+        return sk, perm, [c[perm] for c in companions]
     sorted_keys = torch.empty_like(keys)
     perm = torch.empty(n, dtype=torch.int64, device=keys.device)
     if n == 0:
-        return sorted_keys, perm
+        return sorted_keys, perm, [c[perm] if o is None else o for c, o in zip(companions, outs)]
+    args = []
+    for j in range(2):
+        if j < len(fused):
+            src, dst = fused[j]
+            args += [dptr(src), dptr(dst), src.element_size()]
+        else:
+            args += [None, None, 0]
     ws = _lib.workspace(ws_bytes, keys.device)
-    check(lib.ogn_sort_rows(dptr(keys), n, max_key, dptr(sorted_keys), dptr(perm), dptr(ws), ws_bytes,
+    check(lib.ogn_sort_rows(dptr(keys), n, max_key, dptr(sorted_keys), dptr(perm), *args, dptr(ws), ws_bytes,
                             stream_of(keys)), "sort_rows")
-    return sorted_keys, perm
+    return sorted_keys, perm, [c[perm] if o is None else o for c, o in zip(companions, outs)]
 
 
 def index_facts(index: torch.Tensor, key: Optional[torch.Tensor] = None) -> Tuple[bool, int, int]:

@@ -258,11 +258,11 @@ class _Csr:
         perm = self.perm
         if perm is None:
             # columns lie in [0, n) (validated with the CSR): bounded-key sort
-            sorted_col, perm = _native.sort_rows(self.col, max(self.n - 1, 0))
+            sorted_col, perm, (row_t,) = _native.sort_rows(self.col, max(self.n - 1, 0), (row,))
         else:
-            sorted_col = self.col[perm]
+            sorted_col, row_t = self.col[perm], row[perm]
         colptr = self.colptr if self.colptr is not None else _C.convert(sorted_col, self.n + 1, True)
-        return colptr, row[perm], perm
+        return colptr, row_t, perm
 
 
 # ---------------------------------------------------------------- autograd
@@ -404,29 +404,31 @@ def csr_spmm(rowptr: torch.Tensor, col: torch.Tensor, value: Optional[torch.Tens
     return (out, arg) if r >= 2 else out
 
 
-def _coo_layout_uncached(index: torch.Tensor, m: int):
-    """(ptr, col, perm or None) of a COO index [2, E]; rows ordered stably.
-    One device probe gives the row range and sortedness together."""
+def _coo_layout_uncached(index: torch.Tensor, m: int, value: Optional[torch.Tensor] = None):
+    """(ptr, col, perm or None, value in row order or None) of a COO index
+    [2, E]; rows ordered stably.  One device probe gives the row range and
+    sortedness together; the columns (and a 1-D 4- or 8-byte value) are
+    permuted inside the sort's last pass."""
     row = index[0]
     if row.numel() == 0:
-        return torch.zeros(m + 1, dtype=torch.int64, device=index.device), index[1].clone(), None
+        return (torch.zeros(m + 1, dtype=torch.int64, device=index.device), index[1].clone(), None,
+                None if value is None else value.clone())
     unsorted, lo, hi = _native.index_probe(row)
     if lo < 0 or hi >= m:
         raise ValueError("COO row out of range")
     if not unsorted:
-        return _C.convert(row, m + 1, True), index[1].clone(), None
-    sorted_row, perm = _native.sort_rows(row, m - 1)
-    return _C.convert(sorted_row, m + 1, True), index[1][perm], perm
+        return _C.convert(row, m + 1, True), index[1].clone(), None, None if value is None else value.clone()
+    carried = (index[1],) if value is None else (index[1], value)
+    sorted_row, perm, outs = _native.sort_rows(row, m - 1, carried)
+    return _C.convert(sorted_row, m + 1, True), outs[0], perm, None if value is None else outs[1]
 
 
 def coo_to_csr(index: torch.Tensor, value: Optional[torch.Tensor], m: int
                ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """COO [2, E] -> (rowptr, col, value) with columns stably ordered by row;
     nothing is cached (reference :284-294)."""
-    ptr, col, perm = _coo_layout_uncached(index, m)
-    if value is None:
-        return ptr, col, None
-    return ptr, col, value.clone() if perm is None else value[perm]
+    ptr, col, _, vals = _coo_layout_uncached(index, m, value)
+    return ptr, col, vals
 
 
 def _coo_layout(index: torch.Tensor, m: int):
@@ -434,7 +436,7 @@ def _coo_layout(index: torch.Tensor, m: int):
     hit = _COO_LAYOUTS.lookup((index,), (m,))
     if hit is not _MISS:
         return hit
-    layout = _coo_layout_uncached(index, m)
+    layout = _coo_layout_uncached(index, m)[:3]
     _COO_LAYOUTS.store((index,), (m,), layout)
     return layout
 

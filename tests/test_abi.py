@@ -78,8 +78,18 @@ def test_sort_rows_refuses_out_of_range_sizes_without_gpu():
     # checked before any device work
     import ops_gnn._lib as L
 
-    assert L.lib.ogn_sort_rows(None, 2**31, 10, None, None, None, 0, None) == 2  # OGN_EUNSUPPORTED
-    assert L.lib.ogn_sort_rows(None, 10, 2**32, None, None, None, 0, None) == 2
-    assert L.lib.ogn_sort_rows(None, -1, 10, None, None, None, 0, None) == 1  # OGN_EINVAL
-    assert L.lib.ogn_sort_rows(None, 0, 10, None, None, None, 0, None) == 0  # nothing to sort
-    assert L.lib.ogn_sort_rows_workspace_size(2**31, 10) == 0
+    assert L.lib.ogn_sort_rows(None, 2**31, 10, None, None, None, None, 0, None, None, 0, None, 0, None) == 2  # OGN_EUNSUPPORTED
+    assert L.lib.ogn_sort_rows(None, 10, 2**32, None, None, None, None, 0, None, None, 0, None, 0, None) == 2
+    assert L.lib.ogn_sort_rows(None, -1, 10, None, None, None, None, 0, None, None, 0, None, 0, None) == 1  # OGN_EINVAL
+    assert L.lib.ogn_sort_rows(None, 0, 10, None, None, None, None, 0, None, None, 0, None, 0, None) == 0  # nothing to sort
+    assert L.lib.ogn_sort_rows(None, 10, 5, None, None, None, None, 2, None, None, 0, None, 0, None) == 1
+    assert L.lib.ogn_sort_rows_workspace_size(2**31, 10, 0, 0) == 0
+
+
+def test_sort_rows_companion_rules_without_gpu():
+    import ops_gnn._lib as L
+
+    # companion b without a, and a width other than 4 / 8: refused before any device work
+    assert L.lib.ogn_sort_rows(None, 10, 5, None, None, None, None, 0, None, None, 4, None, 0, None) == 1
+    assert L.lib.ogn_sort_rows_workspace_size(10, 5, 0, 4) == 0
+    assert L.lib.ogn_sort_rows_workspace_size(10, 5, 2, 0) == 0
