@@ -166,6 +166,29 @@ def test_config3_spmm_sum_bf16_full_size(ogn, oracle, cfg3):
     assert float(err.max()) <= 0, f"config-3 bf16 C w differs from A (B w): worst excess {float(err.max()):.3e}"
 
 
+def test_config3_coo_to_csr_full_size(ogn, cfg3):
+    # config 3's 62 M edges in random order back to CSR through the
+    # torch_sparse frontend: row pointers equal the original, and the columns
+    # and values come out in the order of a stable argsort of the rows
+    # (the reference's, python/ops_gnn/torch_sparse_spmm.py:273-342), bit for bit
+    from ops_gnn import torch_sparse_spmm as tss
+    from ops_gnn.convert import ptr2ind_tensor
+
+    _, d = cfg3
+    ptr, col, val = d["ptr"], d["col"], d["val"]
+    e, m = col.numel(), ptr.numel() - 1
+    order = torch.randperm(e, device=DEV, generator=torch.Generator(device=DEV).manual_seed(11))
+    row = ptr2ind_tensor(ptr, e)
+    index = torch.stack([row[order], col[order]]).contiguous()
+    value = val[order].contiguous()
+    del row
+    got_ptr, got_col, got_val = tss.coo_to_csr(index, value, m)
+    assert torch.equal(got_ptr, ptr)
+    perm = torch.sort(index[0], stable=True)[1]
+    assert torch.equal(got_col, index[1][perm])
+    assert torch.equal(got_val, value[perm])
+
+
 def test_config2_segment_full_size(ogn, oracle):
     from ops_gnn.synthetic import cfg2_segments
 
