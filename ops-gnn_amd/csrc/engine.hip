@@ -32,15 +32,15 @@ Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned, bool ga
     pl.g = 64;
     pl.tiles = (k + 63) / 64;
   }
-  // Feature traffic per wave, in whole 64-position windows: 64 KiB in
-  // contiguous mode (short rows: more, shorter chunks keep the tail small;
-  // config 5 scatter at 256 / 384 / 512 / 1024 positions: sum 1.47 / 1.47 /
-  // 1.42 / 1.46 ms, logsumexp 2.11 / 2.01 / 1.98 / 2.05 ms), 256 KiB in
+  // Feature traffic per wave, in whole 64-position windows: 48 KiB in
+  // contiguous mode (config 5 scatter, wall ms, at 320 / 384 / 448 / 512
+  // positions: sum 1.166 / 1.168 / 1.176 / 1.184, max 1.315 / 1.314 / 1.315 /
+  // 1.329, logsumexp 1.198 / 1.191 / 1.202 / 1.221), 256 KiB in
   // gather mode, where halving the chunk count halves the rows that cross a
   // chunk boundary and so the fix-up pass (config 3 SpMM sum step 5.79 ->
   // 5.70 ms, max 7.27 -> 6.96 ms).
   const int64_t row_bytes = std::max<int64_t>(1, std::min<int64_t>(k, 64 * vec) * esz);
-  int64_t wave_bytes = gather ? 262144 : 65536;
+  int64_t wave_bytes = gather ? 262144 : 49152;
   if (const char* env = std::getenv("OGN_ENGINE_WAVE_KIB")) {
     const long v = std::atol(env);
     if (v >= 16) wave_bytes = (int64_t)v * 1024;
@@ -54,7 +54,17 @@ Plan make_plan(int64_t nnz_bound, int64_t k, int in_dtype, bool aligned, bool ga
   // SIMD), so latency is hidden (floor 128 positions: smaller chunks cost
   // more in row fix-ups than they gain).
   const int64_t waves_floor = ((nnz_bound / 8192) / 64) * 64;
-  if (!std::getenv("OGN_ENGINE_CHUNK")) chunk = std::min<int64_t>(chunk, std::max<int64_t>(waves_floor, 128));
+  if (!std::getenv("OGN_ENGINE_CHUNK")) {
+    chunk = std::min<int64_t>(chunk, std::max<int64_t>(waves_floor, 128));
+    // Contiguous mode, fewer than two rounds of resident waves (4096 = 256
+    // CUs x 16): one round instead -- no partly filled second round, and
+    // half the rows crossing chunk ends (config 2: 7812 waves of 128
+    // positions -> 3906 of 256; segment max 140 -> 131 us and 150 -> 145 us
+    // on two boxes, sum and logsumexp within 1 %).
+    constexpr int64_t kRound = 4096;
+    if (!gather && nnz_bound > 0 && (nnz_bound + chunk - 1) / chunk < 2 * kRound)
+      chunk = std::max<int64_t>(chunk, ((nnz_bound + kRound - 1) / kRound + 63) / 64 * 64);
+  }
   pl.chunk = std::min<int64_t>(std::max<int64_t>(chunk, 64), 8192);
   pl.nchunks = std::max<int64_t>(1, (nnz_bound + pl.chunk - 1) / pl.chunk);
   return pl;
