@@ -272,6 +272,25 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
                        int64_t* arg, int reduce, int semantics, int flags, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* ogn_segment_reduce over rows read through an index: position i of the
+ * segments (indptr, int64 [segments + 1], as ogn_segment_reduce with one
+ * batch) is row rows[i] of src [src_rows, k]; torch_scatter semantics only
+ * (OGN_SEM_SCATTER: flags OGN_SEG_HAS_OUT seeds from out; min/max take the
+ * LATER position on ties, in `rows` order), float32 / float16 / bfloat16,
+ * reduce sum, mean, min, max or prod.  arg (optional, min/max) gets the src
+ * row of each winner (rows[i]), src_rows when nothing was taken.  The
+ * unsorted scatter sorts its index stably (ogn_sort_rows) and reduces here,
+ * so that every output row is folded by one wavefront schedule instead of
+ * contended atomics (reference scatter_kernel_atomic.h:338-412 and the arg
+ * pass scatter_kernel_minmax.h:120-175 for the same operation).  Workspace:
+ * ogn_segment_reduce_gather_workspace_size. */
+size_t ogn_segment_reduce_gather_workspace_size(int64_t length, int64_t segments, int64_t k, int dtype,
+                                                int reduce);
+int ogn_segment_reduce_gather(const int64_t* indptr, const int64_t* rows, const void* src, int dtype,
+                              int64_t src_rows, int64_t length, int64_t segments, int64_t k, void* out,
+                              int64_t* arg, int reduce, int semantics, int flags, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* Batched ind2ptr over int64 sorted indices: ind [batches, numel] ->
  * out [batches, rows + 1].  Used to turn a sorted COO index into segment
  * pointers (reference segment_coo BuildPointers,

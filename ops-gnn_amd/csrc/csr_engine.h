@@ -1559,13 +1559,13 @@ void launch_rk_f(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
 
 // Which variant serves a request: the fast ones need x * w messages with a
 // scalar (or no) weight, no product reduction, and for min/max the
-// NaN-ignoring first-tie rule (torch_sparse SpMM, segment_csr) or, in
-// contiguous mode, the later-tie rule (segment_coo, sorted scatter).
+// NaN-ignoring first-tie rule (torch_sparse SpMM, segment_csr) or the
+// later-tie rule (segment_coo, scatter).
 inline int variant_of(int rk, bool gather, const Params& p) {
   if (p.val_op != OP_MUL || p.val_mode == 2 || p.reduce == OGN_REDUCE_PROD) return V_GENERIC;
   if (rk != RK_MINMAX) return V_FIRST;
   if (p.mm_mode == MM_SPMM || p.mm_mode == MM_SEGCSR) return V_FIRST;
-  if (!gather && p.mm_mode == MM_LATER) return V_LATER;
+  if (p.mm_mode == MM_LATER) return V_LATER;
   return V_GENERIC;
 }
 
@@ -1580,7 +1580,9 @@ void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
       return;
     }
   }
-  if constexpr (!GATHER && RK == RK_MINMAX) {
+  // later-tie extrema: contiguous segments, and gather mode with int64 rows
+  // (the unsorted scatter reducing through its sort permutation)
+  if constexpr (RK == RK_MINMAX && (!GATHER || std::is_same<IDX, int64_t>::value)) {
     if (v == V_LATER) {
       launch_rk_f<DT, IDX, RK, GATHER, V_LATER>(pl, grid, s, p);
       return;

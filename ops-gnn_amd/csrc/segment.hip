@@ -975,6 +975,78 @@ int ogn_segment_reduce(const int64_t* indptr, int64_t ptr_batches, const void* s
              static_cast<hipStream_t>(stream), "segment", layout);
 }
 
+// arg[j] = rows[arg[j]] for a winning position, unchanged (the empty marker) otherwise.
+__global__ __launch_bounds__(256) void map_arg_kernel(int64_t* __restrict__ arg, int64_t cells,
+                                                      const int64_t* __restrict__ rows, int64_t length) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cells; i += stride) {
+    const int64_t a = arg[i];
+    if (a >= 0 && a < length) arg[i] = rows[a];
+  }
+}
+
+size_t ogn_segment_reduce_gather_workspace_size(int64_t length, int64_t segments, int64_t k, int dtype,
+                                                int reduce) {
+  if (length < 0 || segments < 0 || k <= 0 || is_exact_dtype(dtype)) return 0;
+  const int rk = rk_of(reduce);
+  const Plan pa = make_plan(length, k, dtype, true, true);
+  const Plan pu = make_plan(length, k, dtype, false, true);
+  return std::max(workspace_layout(pa, k, 1, 1, rk).total, workspace_layout(pu, k, 1, 1, rk).total);
+}
+
+int ogn_segment_reduce_gather(const int64_t* indptr, const int64_t* rows, const void* src, int dtype,
+                              int64_t src_rows, int64_t length, int64_t segments, int64_t k, void* out,
+                              int64_t* arg, int reduce, int semantics, int flags, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (src_rows < 0 || length < 0 || segments < 0 || k < 0)
+    return fail(OGN_EINVAL, "ogn_segment_reduce_gather: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_segment_reduce_gather: src dtype must be float32, float16 or bfloat16");
+  if (reduce < OGN_REDUCE_SUM || reduce > OGN_REDUCE_PROD)
+    return fail(OGN_EUNSUPPORTED, "ogn_segment_reduce_gather: sum, mean, min, max or prod");
+  if (semantics != OGN_SEM_SCATTER) return fail(OGN_EUNSUPPORTED, "ogn_segment_reduce_gather: scatter semantics");
+  if (segments == 0 || k == 0) return OGN_OK;
+  if (!indptr || !out || (length > 0 && (!rows || !src)))
+    return fail(OGN_EINVAL, "ogn_segment_reduce_gather: null pointer");
+  if (length > 0 && src_rows == 0) return fail(OGN_EINVAL, "ogn_segment_reduce_gather: positions need src rows");
+  const bool has_out = (flags & OGN_SEG_HAS_OUT) != 0;
+  const int rk = rk_of(reduce);
+  const bool aligned = is_aligned(src, 16) && is_aligned(out, 16);
+  const Plan pl = make_plan(length, k, dtype, aligned, true);
+  Params p{};
+  p.ptr = indptr;
+  p.ptr_bstride = 0;
+  p.col = rows;
+  p.src = src;
+  p.src_dt = dtype;
+  p.src_bstride = 0;
+  p.out = out;
+  p.out_dt = dtype;
+  p.out_bstride = segments * k;
+  p.arg = arg;
+  p.m = segments;
+  p.n = std::max<int64_t>(src_rows, 1);
+  p.k = k;
+  p.nnz_bound = length;
+  p.reduce = reduce;
+  p.arg_empty = src_rows;
+  // torch_scatter rules, as ogn_segment_reduce with OGN_SEM_SCATTER
+  p.mm_mode = MM_LATER;
+  p.seed_mode = has_out ? SEED_OUT : SEED_LIMIT;
+  p.sum_seed = has_out;
+  p.mean_keep_empty = has_out;
+  p.limit = dtype == OGN_F32 ? 3.4028234663852886e38f : (dtype == OGN_F16 ? 65504.f : 3.3895313892515355e38f);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rc = run(pl, p, dtype, OGN_I64, true, rk, 1, workspace, workspace_bytes, s, "segment_gather", 0);
+  if (rc != OGN_OK || !arg || rk != RK_MINMAX || length == 0) return rc;
+  // the engine's argument is a position in `rows` order; report the src row
+  const int64_t cells = segments * k;
+  TimedLaunch t("segment_gather_arg", s);
+  hipLaunchKernelGGL(map_arg_kernel, dim3((unsigned)std::min<int64_t>((cells + 255) / 256, 4096)), dim3(256), 0, s,
+                     arg, cells, rows, length);
+  return check_launch("ogn_segment_reduce_gather");
+}
+
 int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, int64_t batch, int64_t length,
                             int64_t segments, int64_t k, float* m_out, float* s_out, void* workspace,
                             size_t workspace_bytes, void* stream) {

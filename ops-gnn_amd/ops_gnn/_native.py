@@ -261,6 +261,50 @@ def segment_reduce(src3: torch.Tensor, ptr2d: torch.Tensor, segments: int, reduc
     return out3, arg
 
 
+def segment_reduce_gather(ptr: torch.Tensor, rows: torch.Tensor, src2: torch.Tensor, segments: int, reduce: int,
+                          out2: torch.Tensor, has_out: bool, need_arg: bool) -> Optional[torch.Tensor]:
+    """Scatter-semantics segment reduction over src2 [n, k] rows read through
+    `rows` (include/ogn.h ogn_segment_reduce_gather): segment s covers
+    positions ptr[s] .. ptr[s+1] - 1, position i being src2[rows[i]].
+    Writes out2 [segments, k]; returns the arg (src rows) for min / max."""
+    n, k = src2.shape
+    length = rows.numel()
+    code = _lib.TORCH_TO_OGN[src2.dtype]
+    arg = torch.empty((segments, k), dtype=torch.int64, device=src2.device) if need_arg else None
+    ws_bytes = lib.ogn_segment_reduce_gather_workspace_size(length, segments, k, code, reduce)
+    ws = _lib.workspace(ws_bytes, src2.device)
+    rc = lib.ogn_segment_reduce_gather(dptr(ptr), dptr(rows), dptr(src2), code, n, length, segments, k, dptr(out2),
+                                       dptr(arg), reduce, _lib.SEM_SCATTER, _lib.SEG_HAS_OUT if has_out else 0,
+                                       dptr(ws), ws_bytes, stream_of(src2))
+    check(rc, "scatter (sorted gather)")
+    return arg
+
+
+_SORTED_LAYOUTS = None
+
+
+def sorted_layout(line: torch.Tensor, size: int, key: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(ptr [size + 1], perm) of an unsorted 1-D index with values in
+    [0, size): the stable sort's permutation and the segment pointers of the
+    sorted index, cached per version of `key` (the caller's index tensor)."""
+    global _SORTED_LAYOUTS
+    if _SORTED_LAYOUTS is None:
+        _SORTED_LAYOUTS = _VersionCache(limit=4)
+
+    def compute():
+        keys = line.contiguous()
+        if keys.dtype != torch.int64:
+            keys = keys.to(torch.int64)
+        sorted_keys, perm, _ = sort_rows(keys, max(size - 1, 0))
+        ptr = ind2ptr_batched(sorted_keys.reshape(1, -1), size).reshape(-1)
+        return ptr, perm
+
+    per_size = _SORTED_LAYOUTS.get(key, dict)  # {size: (ptr, perm)} for this index version
+    if size not in per_size:
+        per_size[size] = compute()
+    return per_size[size]
+
+
 def ind2ptr_batched(index2d: torch.Tensor, rows: int) -> torch.Tensor:
     ib, numel = index2d.shape
     out = torch.empty((ib, rows + 1), dtype=torch.int64, device=index2d.device)
