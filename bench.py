@@ -638,7 +638,15 @@ def bench_coo(args):
               sb + 8 * nodes * f),
              ("scatter_log_softmax", lambda: ops_gnn.scatter_log_softmax(src, index, 0, nodes),
               8 * e * f + 8 * e),
-             ("scatter_logsumexp", lambda: ops_gnn.scatter_logsumexp(src, index, 0, nodes), sb)]
+             ("scatter_logsumexp", lambda: ops_gnn.scatter_logsumexp(src, index, 0, nodes), sb),
+             # the same edges in a random order: the unsorted path (index sort
+             # cached after the first call, then the engine through the permutation)
+             ("scatter_sum_unsorted", lambda: ops_gnn.scatter(src_sh, index_sh, 0, dim_size=nodes, reduce="sum"), sb),
+             ("scatter_max_unsorted", lambda: ops_gnn.scatter(src_sh, index_sh, 0, dim_size=nodes, reduce="max"),
+              sb + 8 * nodes * f)]
+    order = torch.randperm(e, device=dev, generator=torch.Generator(device=dev).manual_seed(5))
+    index_sh, src_sh = index[order].contiguous(), src[order].contiguous()
+    del order
     ops = {}
     with torch.no_grad():
         for name, fn, nbytes in cases:

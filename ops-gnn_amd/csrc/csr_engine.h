@@ -552,9 +552,10 @@ void engine_kernel(Params p) {
   // Steps in flight per wave: fewer for the wider min/max and log-sum-exp state.
   constexpr int kUnroll = RK == RK_SUM ? (DT == OGN_F32 ? kUnrollSum32 : kUnrollSum) : kUnrollWide;
   // min/max of weighted fp32 messages compare exact fp64 products (fp16/bf16
-  // products are exact in fp32); contiguous mode has no weights, so its fp32
+  // products are exact in fp32); contiguous mode and the later-tie gather
+  // variant (scatter through a permutation) have no weights, so their fp32
   // comparisons are exact as they are.
-  using MT = std::conditional_t<RK == RK_MINMAX && DT == OGN_F32 && GATHER, double, float>;
+  using MT = std::conditional_t<RK == RK_MINMAX && DT == OGN_F32 && GATHER && VAR != V_LATER, double, float>;
 
   const int lane = lane_id();
   const int sub = lane / G;
@@ -1565,7 +1566,7 @@ inline int variant_of(int rk, bool gather, const Params& p) {
   if (p.val_op != OP_MUL || p.val_mode == 2 || p.reduce == OGN_REDUCE_PROD) return V_GENERIC;
   if (rk != RK_MINMAX) return V_FIRST;
   if (p.mm_mode == MM_SPMM || p.mm_mode == MM_SEGCSR) return V_FIRST;
-  if (p.mm_mode == MM_LATER) return V_LATER;
+  if (p.mm_mode == MM_LATER) return gather && p.val_mode != 0 ? V_GENERIC : V_LATER;  // V_LATER: unweighted
   return V_GENERIC;
 }
 
