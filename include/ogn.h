@@ -291,6 +291,16 @@ int ogn_segment_reduce_gather(const int64_t* indptr, const int64_t* rows, const 
                               int64_t* arg, int reduce, int semantics, int flags, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* ogn_segment_group_stats over rows read through an index (one batch):
+ * position i of the groups (indptr [segments + 1]) is row rows[i] of src
+ * [src_rows, k].  The grouped softmax / logsumexp over an unsorted index
+ * sort it (ogn_sort_rows) and take their statistics here instead of with
+ * contended atomics.  Workspace: ogn_segment_reduce_gather_workspace_size
+ * with reduce = OGN_REDUCE_LSE. */
+int ogn_segment_group_stats_gather(const int64_t* indptr, const int64_t* rows, const void* src, int dtype,
+                                   int64_t src_rows, int64_t length, int64_t segments, int64_t k, float* m_out,
+                                   float* s_out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Batched ind2ptr over int64 sorted indices: ind [batches, numel] ->
  * out [batches, rows + 1].  Used to turn a sorted COO index into segment
  * pointers (reference segment_coo BuildPointers,

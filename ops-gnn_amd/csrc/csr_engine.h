@@ -1593,11 +1593,17 @@ void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
   else launch_rk_f<DT, IDX, RK, GATHER, V_GENERIC>(pl, grid, s, p);
 }
 
-// Gather mode (SpMM) instantiates int32 and int64 indices with sum / min-max;
-// contiguous mode (segments) uses int64 pointers with every reduction kind.
+// Gather mode (SpMM, and scatter / grouped statistics through a permutation)
+// instantiates int32 and int64 indices with sum / min-max and int64 rows for
+// log-sum-exp; contiguous mode (segments) uses int64 pointers with every
+// reduction kind.
 template <int DT>
 void launch_gather_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
-  if (rk == RK_MINMAX) {
+  if (rk == RK_LSE) {
+    // log-sum-exp statistics through a permutation (int64 rows, unweighted):
+    // the grouped softmax over an unsorted index
+    launch_rk_f<DT, int64_t, RK_LSE, true, V_FIRST>(pl, grid, s, p);
+  } else if (rk == RK_MINMAX) {
     i64 ? launch_rk<DT, int64_t, RK_MINMAX, true>(pl, grid, s, p)
         : launch_rk<DT, int32_t, RK_MINMAX, true>(pl, grid, s, p);
   } else {

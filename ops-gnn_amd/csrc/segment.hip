@@ -1087,6 +1087,39 @@ int ogn_segment_group_stats(const int64_t* indptr, const void* src, int dtype, i
              static_cast<hipStream_t>(stream), "segment_stats");
 }
 
+int ogn_segment_group_stats_gather(const int64_t* indptr, const int64_t* rows, const void* src, int dtype,
+                                   int64_t src_rows, int64_t length, int64_t segments, int64_t k, float* m_out,
+                                   float* s_out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (src_rows < 0 || length < 0 || segments < 0 || k < 0)
+    return fail(OGN_EINVAL, "ogn_segment_group_stats_gather: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_segment_group_stats_gather: src dtype must be float32, float16 or bfloat16");
+  if (segments == 0 || k == 0) return OGN_OK;
+  if (!indptr || !m_out || !s_out || (length > 0 && (!rows || !src)))
+    return fail(OGN_EINVAL, "ogn_segment_group_stats_gather: null pointer");
+  if (length > 0 && src_rows == 0) return fail(OGN_EINVAL, "ogn_segment_group_stats_gather: positions need src rows");
+  const bool aligned = is_aligned(src, 16) && is_aligned(m_out, 16);
+  const Plan pl = make_plan(length, k, dtype, aligned, true);
+  Params p{};
+  p.ptr = indptr;
+  p.col = rows;
+  p.src = src;
+  p.src_dt = dtype;
+  p.src_bstride = 0;
+  p.out = m_out;
+  p.out_dt = OGN_F32;
+  p.out_bstride = segments * k;
+  p.aux = s_out;
+  p.m = segments;
+  p.n = std::max<int64_t>(src_rows, 1);
+  p.k = k;
+  p.nnz_bound = length;
+  p.reduce = OGN_REDUCE_LSE;
+  p.arg_empty = src_rows;
+  return run(pl, p, dtype, OGN_I64, true, RK_LSE, 1, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+             "segment_stats_gather");
+}
+
 // Workspace: the long-row list (header + capacity), then the kept plan
 // (counts and cursors, 256 bytes, then 16 bytes of bounds per segment).
 static size_t softmax_list_bytes(int64_t batch, int64_t length, int64_t segments, int vec) {

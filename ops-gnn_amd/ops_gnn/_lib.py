@@ -73,6 +73,7 @@ SIGNATURES = {
     "ogn_index_facts": (_int, [_vp, _i64, _vp, _vp]),
     "ogn_sort_rows_workspace_size": (_sz, [_i64, _i64, _int, _int]),
     "ogn_segment_reduce_gather_workspace_size": (_sz, [_i64, _i64, _i64, _int, _int]),
+    "ogn_segment_group_stats_gather": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "ogn_segment_reduce_gather": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _int,
                                          _vp, _sz, _vp]),
     "ogn_sort_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _sz, _vp]),

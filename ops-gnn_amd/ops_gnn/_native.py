@@ -282,6 +282,10 @@ def segment_reduce_gather(ptr: torch.Tensor, rows: torch.Tensor, src2: torch.Ten
 
 _SORTED_LAYOUTS = None
 
+# Unsorted scatters and grouped statistics over at least this many positions
+# sort their index and reduce through the permutation; smaller ones use atomics.
+SORT_PATH_MIN_LENGTH = 1 << 16
+
 
 def sorted_layout(line: torch.Tensor, size: int, key: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     """(ptr [size + 1], perm) of an unsorted 1-D index with values in
@@ -502,6 +506,14 @@ def group_stats(src3: torch.Tensor, index: torch.Tensor, groups: int, sorted_ind
         ws = _lib.workspace(ws_bytes, src3.device)
         rc = lib.ogn_segment_group_stats(dptr(ptr), dptr(src3), code, b, length, groups, f, dptr(m), dptr(s),
                                          dptr(ws), ws_bytes, stream_of(src3))
+    elif b == 1 and index.dim() == 1 and length >= SORT_PATH_MIN_LENGTH and length < 2**31 and groups <= 2**32:
+        # unsorted: statistics through the stable sort's permutation (cached
+        # per index version) -- no contended atomics
+        ptr, perm = sorted_layout(index, groups, index)
+        ws_bytes = lib.ogn_segment_reduce_gather_workspace_size(length, groups, f, code, _lib.R_LSE)
+        ws = _lib.workspace(ws_bytes, src3.device)
+        rc = lib.ogn_segment_group_stats_gather(dptr(ptr), dptr(perm), dptr(src3), code, length, length, groups, f,
+                                                dptr(m), dptr(s), dptr(ws), ws_bytes, stream_of(src3))
     else:
         idx = index.contiguous()
         key = torch.empty(m.shape, dtype=torch.int32, device=src3.device)

@@ -133,7 +133,7 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
         ptr = _native.sorted_index_ptr(index, size, line.reshape(1, -1))
         res3, arg3 = _native.segment_reduce(src3, ptr, size, code, _lib.SEM_SCATTER, out3, has_out, is_minmax,
                                             key=ptr)
-    elif (compact and checked and before == 1 and length >= _SORT_MIN_LENGTH and length < 2**31
+    elif (compact and checked and before == 1 and length >= _native.SORT_PATH_MIN_LENGTH and length < 2**31
           and size <= 2**32 and src.dtype in (torch.float32, torch.float16, torch.bfloat16)):
         # unsorted: a stable sort of the index (cached per index version),
         # then every output row folded by the engine through the
@@ -155,11 +155,6 @@ def _scatter_forward(src: torch.Tensor, index: torch.Tensor, dim: int, out: Opti
     elif has_out:
         result = out
     return result, (None if arg3 is None else arg3.reshape(shape))
-
-
-# Unsorted scatters of at least this many positions sort their index and
-# reduce through the permutation; smaller ones use the atomic kernel.
-_SORT_MIN_LENGTH = 1 << 16
 
 
 def scatter_sum(src, index, dim: int = -1, out=None, dim_size=None) -> torch.Tensor:

@@ -99,3 +99,34 @@ def test_gather_reduce_c_abi_arg_is_src_row(ogn):
         for f in range(k):
             best = s[pos, f].max()
             assert a[r, f] == pos[s[pos, f] == best][-1]
+
+
+# ----------------------------------------------------------------- grouped softmax family, unsorted index
+SOFT_TOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 4e-2}  # reference grouped_softmax_golden.py:24-28
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+@pytest.mark.parametrize("feat", [1, 32, 33])
+def test_unsorted_grouped_softmax_sort_path(ogn, oracle, dtype, mode, feat):
+    # statistics through the sort permutation (ogn_segment_group_stats_gather):
+    # hub groups, an empty group, +inf / NaN inside a hub group
+    from _util import cast_like
+
+    rng = np.random.default_rng(feat)
+    groups = 3000
+    idx = _index(feat + 1, groups)
+    src = torch.from_numpy((rng.standard_normal((N, feat)) * 4).astype(np.float32))
+    hub = np.nonzero(idx == 7)[0]
+    src[hub[10], 0] = float("inf")
+    src[hub[20], -1] = float("nan")
+    src = src.to(dtype)
+    fn = {"softmax": ogn.scatter_softmax, "log_softmax": ogn.scatter_log_softmax,
+          "logsumexp": ogn.scatter_logsumexp}[mode]
+    dev_idx = torch.from_numpy(idx).cuda()
+    gold = cast_like(oracle.group_softmax(src, torch.from_numpy(idx), 0, groups, mode), dtype)
+    for call in range(2):  # the second call reuses the cached sort
+        got = fn(src.cuda(), dev_idx, 0, groups).float().cpu().numpy()
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(gold))
+        tol = SOFT_TOL[dtype]
+        np.testing.assert_allclose(got, gold, rtol=tol, atol=tol, equal_nan=True)
