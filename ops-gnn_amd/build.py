@@ -66,7 +66,8 @@ def _stale(src: Path, obj: Path, headers) -> bool:
 def build(jobs: int = 8, verbose: bool = True, incremental: bool = False) -> Path:
     """Compile every source (or, with incremental, those whose object is older
     than the source or any header) and link the library."""
-    sources = sorted(CSRC.glob("*.hip"))
+    # the engine instance files take minutes each: start them first
+    sources = sorted(CSRC.glob("*.hip"), key=lambda f: (not f.name.startswith("engine_"), f.name))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     obj_dir = HERE / "_build"

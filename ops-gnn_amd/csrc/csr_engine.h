@@ -1534,6 +1534,12 @@ OGN_ENGINE_DECL(launch_contig_f32)
 OGN_ENGINE_DECL(launch_contig_f16)
 OGN_ENGINE_DECL(launch_contig_bf16)
 OGN_ENGINE_DECL(launch_gather_i8)
+// gather-mode extrema and log-sum-exp (engine_gather_<dt>_ext.hip; their
+// own translation units, so that the build's longest compile is shorter)
+OGN_ENGINE_DECL(launch_gather_f32_ext)
+OGN_ENGINE_DECL(launch_gather_f16_ext)
+OGN_ENGINE_DECL(launch_gather_bf16_ext)
+OGN_ENGINE_DECL(launch_gather_i8_ext)
 #undef OGN_ENGINE_DECL
 
 template <int DT, typename IDX, bool VL, int RK, bool GATHER, int VAR>
@@ -1598,17 +1604,19 @@ void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
 // log-sum-exp; contiguous mode (segments) uses int64 pointers with every
 // reduction kind.
 template <int DT>
-void launch_gather_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
+void launch_gather_sum_dt(const Plan& pl, bool i64, dim3 grid, hipStream_t s, const Params& p) {
+  i64 ? launch_rk<DT, int64_t, RK_SUM, true>(pl, grid, s, p) : launch_rk<DT, int32_t, RK_SUM, true>(pl, grid, s, p);
+}
+
+template <int DT>
+void launch_gather_ext_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
   if (rk == RK_LSE) {
     // log-sum-exp statistics through a permutation (int64 rows, unweighted):
     // the grouped softmax over an unsorted index
-    launch_rk_f<DT, int64_t, RK_LSE, true, V_FIRST>(pl, grid, s, p);
-  } else if (rk == RK_MINMAX) {
+    if constexpr (DT != OGN_I8) launch_rk_f<DT, int64_t, RK_LSE, true, V_FIRST>(pl, grid, s, p);
+  } else {
     i64 ? launch_rk<DT, int64_t, RK_MINMAX, true>(pl, grid, s, p)
         : launch_rk<DT, int32_t, RK_MINMAX, true>(pl, grid, s, p);
-  } else {
-    i64 ? launch_rk<DT, int64_t, RK_SUM, true>(pl, grid, s, p)
-        : launch_rk<DT, int32_t, RK_SUM, true>(pl, grid, s, p);
   }
 }
 
