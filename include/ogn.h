@@ -423,11 +423,21 @@ int ogn_group_lse_from_stats(const float* m, const float* s, int64_t cells, void
  *    saved = forward src [before, len, after], reduced = forward output and
  *    grad = its gradient, both [before, groups, after]; no workspace.
  * Positions whose index is outside [0, groups) get 0.  fp32 math; group sums
- * use atomics (one per run of equal targets in a wavefront). */
+ * use atomics (one per run of equal targets in a wavefront), unless mode
+ * carries OGN_GROUP_BWD_TOTALS_GIVEN: the workspace then already holds the
+ * group sums T (the unsorted-index path computes them without atomics:
+ * ogn_group_bwd_messages, then ogn_segment_reduce_gather over the index's
+ * sort permutation) and only the elementwise pass runs. */
+enum { OGN_GROUP_BWD_TOTALS_GIVEN = 4 };
 int ogn_group_softmax_backward(const void* saved, const void* grad, const void* reduced, int dtype,
                                const void* index, int index_dtype, int64_t before, int64_t len, int64_t after,
                                int64_t groups, int mode, void* grad_src, float* workspace, size_t workspace_bytes,
                                void* stream);
+/* The terms T sums, per position, in fp32: msg[i] = saved[i] * grad[i]
+ * (mode 0) or grad[i] (mode 1), n elements.  No counterpart in the
+ * reference (its sums are fused atomics). */
+int ogn_group_bwd_messages(const void* saved, const void* grad, int dtype, int64_t n, int mode, float* msg,
+                           void* stream);
 
 /* ------------------------------------------------------------------ gather
  * Expansion of segment rows (raw bytes: any dtype, bit-exact).

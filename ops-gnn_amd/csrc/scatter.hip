@@ -406,6 +406,17 @@ __global__ __launch_bounds__(256) void group_bwd_sum_kernel(GroupBwdArgs a) {
   }
 }
 
+// The per-position terms the backward sums per group, in fp32: out * grad
+// (softmax, mode 0) or grad (log_softmax, mode 1).
+__global__ __launch_bounds__(256) void group_bwd_messages_kernel(const void* saved, const void* grad, int dt, int64_t n,
+                                                                 int mode, float* __restrict__ msg) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gv = load_float(grad, dt, i);
+    msg[i] = mode == 0 ? load_float(saved, dt, i) * gv : gv;
+  }
+}
+
 __global__ __launch_bounds__(256) void group_bwd_apply_kernel(GroupBwdArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -617,6 +628,20 @@ int ogn_group_lse_from_stats(const float* m, const float* s, int64_t cells, void
   return check_launch("ogn_group_lse_from_stats");
 }
 
+int ogn_group_bwd_messages(const void* saved, const void* grad, int dtype, int64_t n, int mode, float* msg,
+                           void* stream) {
+  if (n < 0) return fail(OGN_EINVAL, "ogn_group_bwd_messages: negative size");
+  if (dtype != OGN_F32 && dtype != OGN_F16 && dtype != OGN_BF16)
+    return fail(OGN_EUNSUPPORTED, "ogn_group_bwd_messages: dtype must be float32, float16 or bfloat16");
+  if (mode != 0 && mode != 1) return fail(OGN_EINVAL, "ogn_group_bwd_messages: mode must be 0 or 1");
+  if (n == 0) return OGN_OK;
+  if (!grad || !msg || (mode == 0 && !saved)) return fail(OGN_EINVAL, "ogn_group_bwd_messages: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TimedLaunch t("group_bwd_messages", st);
+  hipLaunchKernelGGL(group_bwd_messages_kernel, dim3(grid_for(n)), dim3(256), 0, st, saved, grad, dtype, n, mode, msg);
+  return check_launch("ogn_group_bwd_messages");
+}
+
 int ogn_group_softmax_backward(const void* saved, const void* grad, const void* reduced, int dtype,
                                const void* index, int index_dtype, int64_t before, int64_t len, int64_t after,
                                int64_t groups, int mode, void* grad_src, float* workspace, size_t workspace_bytes,
@@ -627,6 +652,8 @@ int ogn_group_softmax_backward(const void* saved, const void* grad, const void* 
     return fail(OGN_EUNSUPPORTED, "ogn_group_softmax_backward: dtype must be float32, float16 or bfloat16");
   if (index_dtype != OGN_I32 && index_dtype != OGN_I64)
     return fail(OGN_EINVAL, "ogn_group_softmax_backward: index dtype must be int32 or int64");
+  const bool given = (mode & OGN_GROUP_BWD_TOTALS_GIVEN) != 0;
+  mode &= ~OGN_GROUP_BWD_TOTALS_GIVEN;
   if (mode < 0 || mode > 2) return fail(OGN_EINVAL, "ogn_group_softmax_backward: mode must be 0, 1 or 2");
   const int64_t total = before * len * after;
   if (total == 0) return OGN_OK;
@@ -651,7 +678,7 @@ int ogn_group_softmax_backward(const void* saved, const void* grad, const void* 
   a.total = workspace;
   a.grad_src = grad_src;
   a.mode = mode;
-  if (mode != 2 && cells > 0) {
+  if (mode != 2 && cells > 0 && !given) {
     TimedLaunch t("group_bwd_sum", st);
     hipLaunchKernelGGL(group_zero_kernel, dim3(grid_for(cells)), dim3(256), 0, st, workspace, cells);
     hipLaunchKernelGGL(group_bwd_sum_kernel, dim3(grid_for(total)), dim3(256), 0, st, a);

@@ -74,6 +74,7 @@ SIGNATURES = {
     "ogn_sort_rows_workspace_size": (_sz, [_i64, _i64, _int, _int]),
     "ogn_segment_reduce_gather_workspace_size": (_sz, [_i64, _i64, _i64, _int, _int]),
     "ogn_segment_group_stats_gather": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "ogn_group_bwd_messages": (_int, [_vp, _vp, _int, _i64, _int, _vp, _vp]),
     "ogn_segment_reduce_gather": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _int, _int, _int,
                                          _vp, _sz, _vp]),
     "ogn_sort_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _sz, _vp]),
@@ -104,6 +105,7 @@ SIGNATURES = {
 # reduce / semantics codes (include/ogn.h)
 R_SUM, R_MEAN, R_MIN, R_MAX, R_PROD, R_LSE = range(6)
 SEM_SEGMENT_CSR, SEM_SEGMENT_COO, SEM_SCATTER, SEM_DGL = range(4)
+GROUP_BWD_TOTALS_GIVEN = 4  # ogn_group_softmax_backward: the workspace holds the group sums
 MSG_MUL, MSG_ADD, MSG_SUB, MSG_DIV = range(4)
 SPMM_TORCH_SPARSE, SPMM_DGL = range(2)
 SDDMM_OPS = {"dot": 0, "add": 1, "sub": 2, "mul": 3, "div": 4, "copy_lhs": 5, "copy_rhs": 6}

@@ -557,6 +557,22 @@ def group_softmax_backward(saved3, grad3, index, groups, mode, reduced3=None) ->
         return out
     idx = index.contiguous()
     cells = b * groups * f if mode != 2 else 0
+    code = _lib.TORCH_TO_OGN[saved3.dtype]
+    if (mode != 2 and b == 1 and index.dim() == 1 and length >= SORT_PATH_MIN_LENGTH and length < 2**31
+            and groups <= 2**32):
+        # unsorted index: the group sums through the sort permutation (fp32
+        # terms, then the engine), no contended atomics; then the elementwise pass
+        ptr, perm = sorted_layout(index, groups, index)
+        msg = torch.empty((length, f), dtype=torch.float32, device=saved3.device)
+        check(lib.ogn_group_bwd_messages(dptr(saved3), dptr(grad3), code, length * f, mode, dptr(msg),
+                                         stream_of(saved3)), "group softmax backward")
+        totals = torch.empty((groups, f), dtype=torch.float32, device=saved3.device)
+        segment_reduce_gather(ptr, perm, msg, groups, _lib.R_SUM, totals, False, False)
+        rc = lib.ogn_group_softmax_backward(dptr(saved3), dptr(grad3), None, code, dptr(idx), _index_code(idx), b,
+                                            length, f, groups, mode | _lib.GROUP_BWD_TOTALS_GIVEN, dptr(out),
+                                            dptr(totals), totals.numel() * 4, stream_of(saved3))
+        check(rc, "group softmax backward")
+        return out
     ws = torch.empty(max(cells, 1), dtype=torch.float32, device=saved3.device)
     rc = lib.ogn_group_softmax_backward(dptr(saved3), dptr(grad3), dptr(reduced3), _lib.TORCH_TO_OGN[saved3.dtype],
                                         dptr(idx), _index_code(idx), b, length, f, groups, mode, dptr(out),

@@ -130,3 +130,26 @@ def test_unsorted_grouped_softmax_sort_path(ogn, oracle, dtype, mode, feat):
         np.testing.assert_array_equal(np.isnan(got), np.isnan(gold))
         tol = SOFT_TOL[dtype]
         np.testing.assert_allclose(got, gold, rtol=tol, atol=tol, equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["softmax", "log_softmax", "logsumexp"])
+@pytest.mark.parametrize("feat", [1, 32])
+def test_unsorted_grouped_softmax_backward_sort_path(ogn, oracle, dtype, mode, feat):
+    # the backward's group sums through the sort permutation
+    # (ogn_group_bwd_messages + ogn_segment_reduce_gather, then the
+    # elementwise pass) against the float64 oracle gradient
+    rng = np.random.default_rng(40 + feat)
+    groups = 2000
+    idx = _index(feat + 3, groups)
+    src = torch.from_numpy((rng.standard_normal((N, feat)) * 3).astype(np.float32)).to(dtype)
+    fn = {"softmax": ogn.scatter_softmax, "log_softmax": ogn.scatter_log_softmax,
+          "logsumexp": ogn.scatter_logsumexp}[mode]
+    x = src.cuda().requires_grad_(True)
+    out = fn(x, torch.from_numpy(idx).cuda(), 0, groups)
+    grad = torch.from_numpy(rng.standard_normal(tuple(out.shape)).astype(np.float32)).to(dtype)
+    out.backward(grad.cuda())
+    want = oracle.group_softmax_backward(src, grad, torch.from_numpy(idx), 0, groups, mode)
+    tol = 1e-4 if dtype == torch.float32 else 5e-2
+    scale = np.abs(want).max() + 1.0
+    np.testing.assert_allclose(x.grad.float().cpu().numpy() / scale, want / scale, rtol=0, atol=tol)
