@@ -93,3 +93,28 @@ def test_sort_rows_companion_rules_without_gpu():
     assert L.lib.ogn_sort_rows(None, 10, 5, None, None, None, None, 0, None, None, 4, None, 0, None) == 1
     assert L.lib.ogn_sort_rows_workspace_size(10, 5, 0, 4) == 0
     assert L.lib.ogn_sort_rows_workspace_size(10, 5, 2, 0) == 0
+
+
+def test_gather_reduction_entry_points_refuse_bad_arguments_without_gpu():
+    # checked before any device work
+    import ops_gnn._lib as L
+
+    f32 = L.TORCH_TO_OGN[__import__("torch").float32]
+    i32 = L.TORCH_TO_OGN[__import__("torch").int32]
+    g = L.lib.ogn_segment_reduce_gather
+    # (indptr, rows, src, dtype, src_rows, length, segments, k, out, arg, reduce, semantics, flags, ws, bytes, stream)
+    assert g(None, None, None, f32, -1, 0, 1, 1, None, None, L.R_SUM, L.SEM_SCATTER, 0, None, 0, None) == 1
+    assert g(None, None, None, i32, 1, 1, 1, 1, None, None, L.R_SUM, L.SEM_SCATTER, 0, None, 0, None) == 2
+    assert g(None, None, None, f32, 1, 1, 1, 1, None, None, L.R_LSE, L.SEM_SCATTER, 0, None, 0, None) == 2
+    assert g(None, None, None, f32, 1, 1, 1, 1, None, None, L.R_SUM, L.SEM_SEGMENT_COO, 0, None, 0, None) == 2
+    assert g(None, None, None, f32, 1, 1, 1, 1, None, None, L.R_SUM, L.SEM_SCATTER, 0, None, 0, None) == 1
+    assert g(None, None, None, f32, 1, 1, 0, 1, None, None, L.R_SUM, L.SEM_SCATTER, 0, None, 0, None) == 0
+    s = L.lib.ogn_segment_group_stats_gather
+    assert s(None, None, None, i32, 1, 1, 1, 1, None, None, None, 0, None) == 2
+    assert s(None, None, None, f32, 1, 1, 1, 1, None, None, None, 0, None) == 1
+    m = L.lib.ogn_group_bwd_messages
+    assert m(None, None, f32, 10, 2, None, None) == 1
+    assert m(None, None, i32, 10, 0, None, None) == 2
+    assert m(None, None, f32, 0, 0, None, None) == 0
+    assert L.lib.ogn_segment_reduce_gather_workspace_size(10, 2, 4, i32, L.R_SUM) == 0
+    assert L.lib.ogn_segment_reduce_gather_workspace_size(10, 2, 4, f32, L.R_SUM) > 0
