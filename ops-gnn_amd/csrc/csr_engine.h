@@ -438,7 +438,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
         // all four packets regardless was measured 15 % slower
         const bool ok = e0 + u < z;
         if constexpr (VL) {
-          E::unpack(ok ? load16(srcb + (e0 + u) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+          E::unpack(ok ? load16_once<true>(srcb + (e0 + u) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
         } else {
           x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + kc) : 0.f;
         }
@@ -479,7 +479,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
         float x[kW][NE];
 #pragma unroll
         for (int u = 0; u < kW; ++u) {
-          if constexpr (VL) E::unpack(load16(srcb + (e0 + sub + u * S) * K + kc), x[u]);
+          if constexpr (VL) E::unpack(load16_once<true>(srcb + (e0 + sub + u * S) * K + kc), x[u]);
           else x[u][0] = E::load1(srcb, (e0 + sub + u * S) * K + kc);
         }
 #pragma unroll
@@ -491,7 +491,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
         for (int u = 0; u < kW; ++u) {
           const bool ok = e0 + sub + u * S < z;
           if constexpr (VL) {
-            E::unpack(ok ? load16(srcb + (e0 + sub + u * S) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+            E::unpack(ok ? load16_once<true>(srcb + (e0 + sub + u * S) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
           } else {
             x[u][0] = ok ? E::load1(srcb, (e0 + sub + u * S) * K + kc) : 0.f;
           }
@@ -813,7 +813,7 @@ void engine_kernel(Params p) {
     for (int64_t bi = 0; bi < nb; ++bi) {
       uint4 xr[FU];
 #pragma unroll
-      for (int u = 0; u < FU; ++u) xr[u] = load16(q + u * stride);
+      for (int u = 0; u < FU; ++u) xr[u] = load16_once<true>(q + u * stride);
       q += FU * stride;
       float x[FU][NE];
 #pragma unroll
@@ -950,7 +950,7 @@ void engine_kernel(Params p) {
           if constexpr (OFF32) {
             xr[u] = ok ? load16(reinterpret_cast<const char*>(srcb) + co[u]) : make_uint4(0u, 0u, 0u, 0u);
           } else {
-            xr[u] = ok ? load16(srcb + cc[u] * K + k0) : make_uint4(0u, 0u, 0u, 0u);
+            xr[u] = ok ? load16_once<!GATHER>(srcb + cc[u] * K + k0) : make_uint4(0u, 0u, 0u, 0u);
           }
 #pragma unroll
           for (int i = 0; i < NW; ++i) w[u][i] = ws[u];

@@ -304,6 +304,20 @@ __device__ __forceinline__ int wave_in_block() {
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
+// A 16-byte packet read exactly once (the contiguous source of a segment
+// reduction): a non-temporal load, which streams past the caches.  Reading
+// 544 MB in 136 KB per-wave chunks of 512-byte rows on one MI355X: 91.6 us
+// with plain loads, 81.4 us non-temporal.
+template <bool NT>
+__device__ __forceinline__ uint4 load16_once(const void* p) {
+  if constexpr (NT) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return load16(p);
+  }
+}
 template <typename T>
 __device__ __forceinline__ T load_stream(const T* p) {
   return __builtin_nontemporal_load(p);
