@@ -111,6 +111,7 @@ struct Params {
   int64_t arg_empty;
   float* aux;           // log-sum-exp statistics mode: out <- max, aux <- sum of exp
   int short_rows;       // contiguous fast variants: chunks of short rows take short_chunk
+                        // (1), their finished rows staged in LDS (2)
 };
 
 template <typename MT>
@@ -297,6 +298,9 @@ __device__ __forceinline__ int64_t chunk_row_end(const Params& p, int64_t pb, in
 // rows of 1-2 positions around hub rows) main kernel: sum / max / logsumexp
 // 1.28 / 1.53 / 1.46 ms with the mean rule alone, 1.24 / 1.41 / 1.28 ms.
 constexpr int64_t kWaveRowMin = 16;
+// LDS words per wave staging short_chunk's finished rows (8 KiB; 32 KiB per
+// block leaves room for the 16 resident waves per CU the engine targets)
+constexpr int kStageWords = 2048;
 __device__ __forceinline__ bool chunk_is_short(int64_t r0, int64_t r_end, int64_t lo, int64_t hi, int S) {
   return r_end - r0 >= 2 || (r_end - r0) * S >= hi - lo;
 }
@@ -335,7 +339,7 @@ constexpr int engine_waves() {
 // argument positions are int32 offsets from the chunk start.
 template <int DT, int G, bool VL, int RK, int VAR, bool MIN>
 __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t lo, int64_t hi, int64_t r0,
-                                            int64_t r_end) {
+                                            int64_t r_end, uint32_t* __restrict__ stage) {
   using E = Elem<DT>;
   using S_t = typename E::S;
   constexpr int NE = VL ? E::VEC : 1;
@@ -360,6 +364,16 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
   // (below), so that one long row does not hold up the sub-groups that fold
   // the short rows dealt beside it.
   const int64_t L = std::max<int64_t>(kWaveRowMin, 2 * (hi - lo) / std::max<int64_t>(1, r_last - r0 + 1));
+  // Finished rows are staged in LDS (p.short_rows == 2) and written kSlots
+  // rows per sub-group at a time, usually once at the end of the chunk.  A
+  // wave's loads and stores share one completion counter here, and with a
+  // store outstanding the compiler can only wait for all of them: a store
+  // after every row made the next row's loads wait for its write as well.
+  constexpr bool kArgs = RK == RK_MINMAX;
+  constexpr int kSlotWords = NE * (kArgs ? 2 : 1);
+  constexpr int kSlots = std::min(32, kStageWords / (kWave * kSlotWords));
+  const bool staged = p.short_rows == 2;
+  int slot = 0;
   auto init = [&](float* acc, float* best, int32_t* barg) {
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
@@ -389,7 +403,8 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
     }
   };
   // Write row r's result (whole row in the chunk) or its head / tail record.
-  auto emit = [&](int64_t r, int64_t rs, int64_t re, const float* acc, const float* best, const int32_t* barg) {
+  auto emit = [&](int64_t r, int64_t rs, int64_t re, const float* acc, const float* best, const int32_t* barg,
+                  int sl) {
     if (re > hi || rs < lo) {
       // partial row: tail if it goes on past the chunk, else head (it began before)
       const bool head = re <= hi;
@@ -413,6 +428,19 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
       for (int i = 0; i < NE; ++i)
         finish_elem<RK, float>(p, b, r, k0 + i, rs, re, acc[i], best[i], barg[i] == kNone32 ? kNone : lo + barg[i],
                                &v[i], &ag[i]);
+      if (sl >= 0) {
+        // staged: values, then (min / max) the argument as an offset from
+        // the chunk start -- every argument of a row inside the chunk lies
+        // in [lo, hi) or is the empty-row value, coded kNone32
+        uint32_t* q = stage + (sl * kWave + lane) * kSlotWords;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) q[i] = __float_as_uint(v[i]);
+        if constexpr (kArgs) {
+#pragma unroll
+          for (int i = 0; i < NE; ++i) q[NE + i] = (uint32_t)(ag[i] == p.arg_empty ? kNone32 : (int32_t)(ag[i] - lo));
+        }
+        return;
+      }
       store_floats<NE, true>(p.out, p.out_dt, off, v);
       if constexpr (RK == RK_MINMAX) {
         if (p.arg) {
@@ -422,7 +450,37 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
       }
     }
   };
+  // Staged rows of this lane's sub-group: slot j holds row gbase + j * S.
+  uint32_t pend = 0;
+  int64_t gbase = r0 + sub;
+  auto flush = [&]() {
+    while (pend) {
+      const int j = __builtin_ctz(pend);
+      pend &= pend - 1;
+      const int64_t off = b * p.out_bstride + (gbase + (int64_t)j * S) * K + k0;
+      const uint32_t* q = stage + (j * kWave + lane) * kSlotWords;
+      float v[NE];
+#pragma unroll
+      for (int i = 0; i < NE; ++i) v[i] = __uint_as_float(q[i]);
+      store_floats<NE, true>(p.out, p.out_dt, off, v);
+      if constexpr (kArgs) {
+        if (p.arg) {
+#pragma unroll
+          for (int i = 0; i < NE; ++i) {
+            const int32_t code = (int32_t)q[NE + i];
+            p.arg[off + i] = code == kNone32 ? p.arg_empty : lo + code;
+          }
+        }
+      }
+    }
+  };
   for (int64_t r = r0 + sub; r <= r_last; r += S) {
+    if (staged && slot == kSlots) {
+      flush();
+      gbase = r;
+      slot = 0;
+    }
+    const int my = slot++;
     const int64_t rs = ptr[r], re = ptr[r + 1];
     if (r == r_end && rs >= hi) break;  // starts in the next chunk
     const int64_t a = std::max<int64_t>(rs, lo), z = std::min<int64_t>(std::min<int64_t>(re, hi), p.n);
@@ -451,8 +509,11 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
       }
     }
     if (!kok) continue;
-    emit(r, rs, re, acc, best, barg);
+    const bool whole = rs >= lo && re <= hi;
+    emit(r, rs, re, acc, best, barg, staged && whole ? my : -1);
+    if (staged && whole) pend |= 1u << my;
   }
+  flush();
   // Long rows: sub-group s folds positions a + s, a + s + S, ... (kW steps
   // in flight), then the sub-group partials are merged in position order.
   constexpr int kW = 8;
@@ -534,7 +595,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
       if constexpr (G <= 8) round(std::integral_constant<int, 8>{});
       if constexpr (G <= 16) round(std::integral_constant<int, 16>{});
       if constexpr (G <= 32) round(std::integral_constant<int, 32>{});
-      if (sub == 0 && kok) emit(r, rs, re, acc, best, barg);
+      if (sub == 0 && kok) emit(r, rs, re, acc, best, barg, -1);
     }
   }
 }
@@ -589,10 +650,12 @@ void engine_kernel(Params p) {
   int64_t r = c == 0 ? 0 : std::min<int64_t>(std::max<int64_t>(p.chunk_row[pb * p.nchunks + c], 0), M - 1);
   if constexpr (!GATHER && FAST) {
     if (p.short_rows) {
+      __shared__ uint32_t stage[kWavesPerBlock * kStageWords];
+      uint32_t* ws = stage + wave_in_block() * kStageWords;
       const int64_t r_end = chunk_row_end(p, pb, c, nce);
       if (chunk_is_short(r, r_end, lo, hi, S)) {
-        if (RK == RK_MINMAX && is_min) short_chunk<DT, G, VL, RK, VAR, true>(p, c, lo, hi, r, r_end);
-        else short_chunk<DT, G, VL, RK, VAR, false>(p, c, lo, hi, r, r_end);
+        if (RK == RK_MINMAX && is_min) short_chunk<DT, G, VL, RK, VAR, true>(p, c, lo, hi, r, r_end, ws);
+        else short_chunk<DT, G, VL, RK, VAR, false>(p, c, lo, hi, r, r_end, ws);
         return;
       }
     }

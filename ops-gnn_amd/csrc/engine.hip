@@ -147,6 +147,7 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
   // contiguous mode, fast variants: chunks of short rows take short_chunk
   p.short_rows = !gather && in_dtype != OGN_I8 && variant_of(rk, false, p) != V_GENERIC &&
                  !std::getenv("OGN_ENGINE_NO_SHORT");
+  if (p.short_rows && !std::getenv("OGN_ENGINE_NO_STAGE")) p.short_rows = 2;
   const KeptKey kl{workspace, p.ptr, {0, p.ptr_bstride, ptr_batches, p.m, p.nnz_bound, pl.chunk, pl.nchunks,
                                        index_dtype}, {}};
   if (!(layout & LAYOUT_REUSE) || !kept_layout_match(kl)) {
