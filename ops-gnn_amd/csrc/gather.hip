@@ -35,6 +35,22 @@ struct GatherArgs {
 
 template <int P>
 struct Packet;
+// Output packets are written once and not read back here: non-temporal
+// stores (config 2 expansion, 512 MB out: 125 -> 89 us).
+template <typename T>
+__device__ __forceinline__ void store_out(T* p, T v) {
+  if constexpr (sizeof(T) == 16) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 q = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(p));
+  } else if constexpr (sizeof(T) == 8) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 q = {v.x, v.y};
+    __builtin_nontemporal_store(q, reinterpret_cast<u32x2*>(p));
+  } else {
+    __builtin_nontemporal_store(v, p);
+  }
+}
 template <> struct Packet<16> { using T = uint4; };
 template <> struct Packet<8> { using T = uint2; };
 template <> struct Packet<4> { using T = uint32_t; };
@@ -112,8 +128,10 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
   const int64_t total = nrows * ppr;
   const T* __restrict__ src = reinterpret_cast<const T*>(a.src + b * a.src_rows * a.row_bytes);
   T* __restrict__ out = reinterpret_cast<T*>(a.out + (b * a.out_rows + i0) * a.row_bytes);
-  // 4 packets per thread per round: all loads issued before the stores
-  constexpr int kU = 4;
+  // 8 packets per thread per round, all loads issued before the stores: a
+  // tile of 512-byte rows is one round, so no load waits behind a store
+  // (with plain stores this alone was 2 % slower than 4 packets)
+  constexpr int kU = 8;
   for (int64_t p0 = threadIdx.x; p0 < total; p0 += kThreads * kU) {
     T v[kU];
     int64_t o[kU];
@@ -132,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u)
-      if (o[u] >= 0) out[o[u]] = v[u];
+      if (o[u] >= 0) store_out(out + o[u], v[u]);
   }
 }
 
