@@ -81,7 +81,10 @@ def build(jobs: int = 8, verbose: bool = True, incremental: bool = False) -> Pat
             f.result()
     target = OUT_DIR / LIB_NAME
     tmp = target.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    # the SONAME lets the extension's dependency on libogn_hip.so resolve to a
+    # copy already loaded from $OGN_LIB, so both routes share one library
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{LIB_NAME}", *map(str, objs),
+           "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
