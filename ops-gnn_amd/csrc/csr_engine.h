@@ -792,6 +792,22 @@ void engine_kernel(Params p) {
     }
   };
 
+  // Gather-mode fp32 sums hold a finished row's result in registers and store it
+  // just after the next batch of gathers is issued: loads and stores share
+  // one completion counter, and a store issued before the gathers made their
+  // wait include its write acknowledgement.
+  constexpr bool DEFER = GATHER && FAST && VL && RK == RK_SUM && DT == OGN_F32;
+  float pv_out[DEFER ? NE : 1];
+  int64_t pv_off = -1;  // -1: nothing pending
+  auto store_pending = [&]() {
+    if constexpr (DEFER) {
+      if (pv_off >= 0) {
+        store_floats<NE, true>(p.out, p.out_dt, pv_off, pv_out);
+        pv_off = -1;
+      }
+    }
+  };
+
   auto flush = [&]() {
     combine();
     if (head_split && first) {
@@ -800,6 +816,18 @@ void engine_kernel(Params p) {
       float v[NE];
       int64_t ag[NE];
       const int64_t off = b * p.out_bstride + r * K + k0;
+      if constexpr (DEFER) {
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+          finish_elem<RK, MT>(p, b, r, k0 + i, rs, re, (float)acc[i], flipv(best[i]), kNone, &v[i], &ag[i]);
+        store_pending();
+#pragma unroll
+        for (int i = 0; i < NE; ++i) pv_out[i] = v[i];
+        pv_off = off;
+        first = false;
+        reset();
+        return;
+      }
       if constexpr (IS_INT && RK == RK_SUM) {
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
@@ -1034,6 +1062,7 @@ void engine_kernel(Params p) {
       if constexpr (WSTEPS > 1) {
         if (wbase + WPOS < hi) stage(wbase + WPOS);  // every step of this window is issued
       }
+      store_pending();
       // Phase 3: consume the steps in order (fully unrolled, so the staged
       // steps stay in registers).
 #pragma unroll
@@ -1111,6 +1140,7 @@ void engine_kernel(Params p) {
     combine();
     write_record(false);
   }
+  store_pending();
 }
 
 // Finish rows that cross chunk boundaries: one wave per chunk that holds the
