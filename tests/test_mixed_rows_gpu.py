@@ -119,3 +119,35 @@ def test_segment_logsumexp_mixed_rows(ogn, oracle, chunk, dtype, feat):
     gold = cast_like(oracle.segment_logsumexp(src, indptr), dtype)
     tol = 1e-5 if dtype == torch.float32 else 1e-2
     np.testing.assert_allclose(got, gold, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("reduce", ["sum", "mean", "min", "max"])
+@pytest.mark.parametrize("feat", [4, 32, 33])
+def test_segment_csr_mixed_rows_batched_pointers(ogn, oracle, chunk, reduce, feat):
+    # one pointer row per batch (different row layouts, the last starting
+    # past position 0): the finished rows of every batch, staged and written
+    # in groups, land in that batch's output
+    rng = np.random.default_rng(40 + feat)
+    n = 6000
+    rows = []
+    for bi in range(3):
+        lengths = _lengths(bi + feat, rows=1500)
+        lead = 0 if bi < 2 else 17
+        lengths = lengths[np.cumsum(lengths) + lead <= n]
+        ptr = np.concatenate([[lead], lead + np.cumsum(lengths)])
+        rows.append(ptr)
+    m = min(r.size for r in rows) - 1
+    indptr = np.stack([r[: m + 1] for r in rows])
+    ties = reduce in ("min", "max")
+    src = _src(rng, 3 * n, feat, torch.float32, ties).reshape(3, n, feat)
+    res = getattr(ogn, f"segment_{reduce}_csr")(src.cuda(), torch.from_numpy(indptr).cuda())
+    out, arg = res if isinstance(res, tuple) else (res, None)
+    for bi in range(3):
+        gold, garg = oracle.segment_csr(src[bi], indptr[bi], reduce)
+        what = f"batched/{chunk}/{reduce}/f{feat}/b{bi}"
+        if ties:
+            assert_exact(out[bi], gold, what + " values")
+            assert_exact(arg[bi], garg, what + " arg")
+        else:
+            scale, _ = oracle.segment_csr(src[bi].abs(), indptr[bi], reduce)
+            assert_sum_close(out[bi], gold, scale, torch.float32, what)
