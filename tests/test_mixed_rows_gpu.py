@@ -151,3 +151,30 @@ def test_segment_csr_mixed_rows_batched_pointers(ogn, oracle, chunk, reduce, fea
         else:
             scale, _ = oracle.segment_csr(src[bi].abs(), indptr[bi], reduce)
             assert_sum_close(out[bi], gold, scale, torch.float32, what)
+
+
+@pytest.mark.parametrize("reduce", ["sum", "max", "logsumexp"])
+@pytest.mark.parametrize("feat", [1, 32, 33])
+def test_staged_and_direct_row_stores_agree(ogn, chunk, reduce, feat):
+    # OGN_ENGINE_NO_STAGE=1 writes each finished short row directly; the
+    # default stages rows in LDS and writes them in groups: same bits
+    lengths = _lengths(50 + feat)
+    rng = np.random.default_rng(60 + feat)
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)])).cuda()
+    src = _src(rng, int(lengths.sum()), feat, torch.float32, reduce == "max").cuda()
+
+    def run():
+        if reduce == "logsumexp":
+            return (ogn.segment_logsumexp(src, indptr),)
+        res = getattr(ogn, f"segment_{reduce}_csr")(src, indptr)
+        return res if isinstance(res, tuple) else (res,)
+
+    staged = run()
+    os.environ["OGN_ENGINE_NO_STAGE"] = "1"
+    try:
+        direct = run()
+    finally:
+        os.environ.pop("OGN_ENGINE_NO_STAGE", None)
+    for a, b in zip(staged, direct):
+        assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a,
+                           b.view(torch.int32) if b.dtype == torch.float32 else b)
