@@ -112,6 +112,7 @@ struct Params {
   float* aux;           // log-sum-exp statistics mode: out <- max, aux <- sum of exp
   int short_rows;       // contiguous fast variants: chunks of short rows take short_chunk
                         // (1), their finished rows staged in LDS (2)
+  int src_nt;           // contiguous source read with non-temporal loads (NTS instances)
 };
 
 template <typename MT>
@@ -337,7 +338,7 @@ constexpr int engine_waves() {
 // s, s + S, ... (eight loads in flight) and the S partials are merged in
 // position order.  The extremum direction is a template parameter, and
 // argument positions are int32 offsets from the chunk start.
-template <int DT, int G, bool VL, int RK, int VAR, bool MIN>
+template <int DT, int G, bool VL, int RK, int VAR, bool MIN, bool NTS>
 __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t lo, int64_t hi, int64_t r0,
                                             int64_t r_end, uint32_t* __restrict__ stage) {
   using E = Elem<DT>;
@@ -496,7 +497,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
         // all four packets regardless was measured 15 % slower
         const bool ok = e0 + u < z;
         if constexpr (VL) {
-          E::unpack(ok ? load16_once<true>(srcb + (e0 + u) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+          E::unpack(ok ? load16_once<NTS>(srcb + (e0 + u) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
         } else {
           x[u][0] = ok ? E::load1(srcb, (e0 + u) * K + kc) : 0.f;
         }
@@ -540,7 +541,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
         float x[kW][NE];
 #pragma unroll
         for (int u = 0; u < kW; ++u) {
-          if constexpr (VL) E::unpack(load16_once<true>(srcb + (e0 + sub + u * S) * K + kc), x[u]);
+          if constexpr (VL) E::unpack(load16_once<NTS>(srcb + (e0 + sub + u * S) * K + kc), x[u]);
           else x[u][0] = E::load1(srcb, (e0 + sub + u * S) * K + kc);
         }
 #pragma unroll
@@ -552,7 +553,7 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
         for (int u = 0; u < kW; ++u) {
           const bool ok = e0 + sub + u * S < z;
           if constexpr (VL) {
-            E::unpack(ok ? load16_once<true>(srcb + (e0 + sub + u * S) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
+            E::unpack(ok ? load16_once<NTS>(srcb + (e0 + sub + u * S) * K + kc) : make_uint4(0u, 0u, 0u, 0u), x[u]);
           } else {
             x[u][0] = ok ? E::load1(srcb, (e0 + sub + u * S) * K + kc) : 0.f;
           }
@@ -600,7 +601,9 @@ __device__ __forceinline__ void short_chunk(const Params& p, int64_t c, int64_t 
   }
 }
 
-template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER, int VAR>
+// NTS: the contiguous source is read with non-temporal loads (chosen per call
+// by its size, see run()).
+template <int DT, typename IDX, int G, bool VL, int RK, bool GATHER, int VAR, bool NTS = false>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(engine_waves<DT, RK, VAR, G, VL>())))
 void engine_kernel(Params p) {
   using E = Elem<DT>;
@@ -654,8 +657,8 @@ void engine_kernel(Params p) {
       uint32_t* ws = stage + wave_in_block() * kStageWords;
       const int64_t r_end = chunk_row_end(p, pb, c, nce);
       if (chunk_is_short(r, r_end, lo, hi, S)) {
-        if (RK == RK_MINMAX && is_min) short_chunk<DT, G, VL, RK, VAR, true>(p, c, lo, hi, r, r_end, ws);
-        else short_chunk<DT, G, VL, RK, VAR, false>(p, c, lo, hi, r, r_end, ws);
+        if (RK == RK_MINMAX && is_min) short_chunk<DT, G, VL, RK, VAR, true, NTS>(p, c, lo, hi, r, r_end, ws);
+        else short_chunk<DT, G, VL, RK, VAR, false, NTS>(p, c, lo, hi, r, r_end, ws);
         return;
       }
     }
@@ -904,7 +907,7 @@ void engine_kernel(Params p) {
     for (int64_t bi = 0; bi < nb; ++bi) {
       uint4 xr[FU];
 #pragma unroll
-      for (int u = 0; u < FU; ++u) xr[u] = load16_once<true>(q + u * stride);
+      for (int u = 0; u < FU; ++u) xr[u] = load16_once<NTS>(q + u * stride);
       q += FU * stride;
       float x[FU][NE];
 #pragma unroll
@@ -1041,7 +1044,7 @@ void engine_kernel(Params p) {
           if constexpr (OFF32) {
             xr[u] = ok ? load16(reinterpret_cast<const char*>(srcb) + co[u]) : make_uint4(0u, 0u, 0u, 0u);
           } else {
-            xr[u] = ok ? load16_once<!GATHER>(srcb + cc[u] * K + k0) : make_uint4(0u, 0u, 0u, 0u);
+            xr[u] = ok ? load16_once<!GATHER && NTS>(srcb + cc[u] * K + k0) : make_uint4(0u, 0u, 0u, 0u);
           }
 #pragma unroll
           for (int i = 0; i < NW; ++i) w[u][i] = ws[u];
@@ -1626,6 +1629,10 @@ OGN_ENGINE_DECL(launch_gather_bf16)
 OGN_ENGINE_DECL(launch_contig_f32)
 OGN_ENGINE_DECL(launch_contig_f16)
 OGN_ENGINE_DECL(launch_contig_bf16)
+// contiguous fast variants with non-temporal source loads (engine_contig_<dt>_nt.hip)
+OGN_ENGINE_DECL(launch_contig_f32_nt)
+OGN_ENGINE_DECL(launch_contig_f16_nt)
+OGN_ENGINE_DECL(launch_contig_bf16_nt)
 OGN_ENGINE_DECL(launch_gather_i8)
 // gather-mode extrema and log-sum-exp (engine_gather_<dt>_ext.hip; their
 // own translation units, so that the build's longest compile is shorter)
@@ -1635,25 +1642,25 @@ OGN_ENGINE_DECL(launch_gather_bf16_ext)
 OGN_ENGINE_DECL(launch_gather_i8_ext)
 #undef OGN_ENGINE_DECL
 
-template <int DT, typename IDX, bool VL, int RK, bool GATHER, int VAR>
+template <int DT, typename IDX, bool VL, int RK, bool GATHER, int VAR, bool NTS = false>
 void launch_g(int g, dim3 grid, hipStream_t s, const Params& p) {
   switch (g) {
 #define OGN_G(GV) \
-  case GV: hipLaunchKernelGGL((engine_kernel<DT, IDX, GV, VL, RK, GATHER, VAR>), grid, dim3(kBlock), 0, s, p); break;
+  case GV: hipLaunchKernelGGL((engine_kernel<DT, IDX, GV, VL, RK, GATHER, VAR, NTS>), grid, dim3(kBlock), 0, s, p); break;
     OGN_G(1) OGN_G(2) OGN_G(4) OGN_G(8) OGN_G(16) OGN_G(32) OGN_G(64)
 #undef OGN_G
     default: break;
   }
 }
 
-template <int DT, typename IDX, int RK, bool GATHER, int VAR>
+template <int DT, typename IDX, int RK, bool GATHER, int VAR, bool NTS = false>
 void launch_rk_f(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
   if (pl.vec) {
-    launch_g<DT, IDX, true, RK, GATHER, VAR>(pl.g, grid, s, p);
+    launch_g<DT, IDX, true, RK, GATHER, VAR, NTS>(pl.g, grid, s, p);
   } else if (pl.g == 1) {
-    hipLaunchKernelGGL((engine_kernel<DT, IDX, 1, false, RK, GATHER, VAR>), grid, dim3(kBlock), 0, s, p);
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 1, false, RK, GATHER, VAR, NTS>), grid, dim3(kBlock), 0, s, p);
   } else {
-    hipLaunchKernelGGL((engine_kernel<DT, IDX, 64, false, RK, GATHER, VAR>), grid, dim3(kBlock), 0, s, p);
+    hipLaunchKernelGGL((engine_kernel<DT, IDX, 64, false, RK, GATHER, VAR, NTS>), grid, dim3(kBlock), 0, s, p);
   }
 }
 
@@ -1669,7 +1676,9 @@ inline int variant_of(int rk, bool gather, const Params& p) {
   return V_GENERIC;
 }
 
-template <int DT, typename IDX, int RK, bool GATHER>
+// NTS (contiguous mode): non-temporal source loads in the fast variants; the
+// generic variant keeps plain loads.
+template <int DT, typename IDX, int RK, bool GATHER, bool NTS = false>
 void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
   const int v = variant_of(RK, GATHER, p);
   if constexpr (GATHER) {
@@ -1684,12 +1693,12 @@ void launch_rk(const Plan& pl, dim3 grid, hipStream_t s, const Params& p) {
   // (the unsorted scatter reducing through its sort permutation)
   if constexpr (RK == RK_MINMAX && (!GATHER || std::is_same<IDX, int64_t>::value)) {
     if (v == V_LATER) {
-      launch_rk_f<DT, IDX, RK, GATHER, V_LATER>(pl, grid, s, p);
+      launch_rk_f<DT, IDX, RK, GATHER, V_LATER, NTS>(pl, grid, s, p);
       return;
     }
   }
-  if (v == V_FIRST) launch_rk_f<DT, IDX, RK, GATHER, V_FIRST>(pl, grid, s, p);
-  else launch_rk_f<DT, IDX, RK, GATHER, V_GENERIC>(pl, grid, s, p);
+  if (v == V_FIRST) launch_rk_f<DT, IDX, RK, GATHER, V_FIRST, NTS>(pl, grid, s, p);
+  else if constexpr (!NTS) launch_rk_f<DT, IDX, RK, GATHER, V_GENERIC>(pl, grid, s, p);
 }
 
 // Gather mode (SpMM, and scatter / grouped statistics through a permutation)
@@ -1713,12 +1722,12 @@ void launch_gather_ext_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream
   }
 }
 
-template <int DT>
+template <int DT, bool NTS = false>
 void launch_contig_dt(const Plan& pl, int rk, bool i64, dim3 grid, hipStream_t s, const Params& p) {
   (void)i64;  // segment pointers are int64
-  if (rk == RK_MINMAX) launch_rk<DT, int64_t, RK_MINMAX, false>(pl, grid, s, p);
-  else if (rk == RK_LSE) launch_rk<DT, int64_t, RK_LSE, false>(pl, grid, s, p);
-  else launch_rk<DT, int64_t, RK_SUM, false>(pl, grid, s, p);
+  if (rk == RK_MINMAX) launch_rk<DT, int64_t, RK_MINMAX, false, NTS>(pl, grid, s, p);
+  else if (rk == RK_LSE) launch_rk<DT, int64_t, RK_LSE, false, NTS>(pl, grid, s, p);
+  else launch_rk<DT, int64_t, RK_SUM, false, NTS>(pl, grid, s, p);
 }
 
 }  // namespace eng

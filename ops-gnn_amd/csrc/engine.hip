@@ -148,6 +148,16 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
   p.short_rows = !gather && in_dtype != OGN_I8 && variant_of(rk, false, p) != V_GENERIC &&
                  !std::getenv("OGN_ENGINE_NO_SHORT");
   if (p.short_rows && !std::getenv("OGN_ENGINE_NO_STAGE")) p.short_rows = 2;
+  // Contiguous fast variants read a source larger than the 256 MiB
+  // last-level cache with non-temporal loads (each packet is read once per
+  // call), a smaller one with plain loads, which leave it cached for the next
+  // call: config 2 (544 MB) segment sum 119 -> 108 us non-temporal; 64 / 128
+  // / 192 MB sources 26 / 31 / 40 us plain against 31 / 34 / 43 us.
+  // OGN_ENGINE_NT=0 / 1 forces either, for A/B measurement.
+  const double src_bytes = (double)batch * (double)p.nnz_bound * (double)p.k * (double)dtype_size(in_dtype);
+  bool nt = src_bytes > 256.0 * 1024 * 1024;
+  if (const char* env = std::getenv("OGN_ENGINE_NT")) nt = std::atoi(env) != 0;
+  p.src_nt = !gather && in_dtype != OGN_I8 && nt && variant_of(rk, false, p) != V_GENERIC;
   const KeptKey kl{workspace, p.ptr, {0, p.ptr_bstride, ptr_batches, p.m, p.nnz_bound, pl.chunk, pl.nchunks,
                                        index_dtype}, {}};
   if (!(layout & LAYOUT_REUSE) || !kept_layout_match(kl)) {
@@ -163,16 +173,19 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
     TimedLaunch t((n + "_main").c_str(), s);
     switch (in_dtype) {
       case OGN_F32:
-        gather ? launch_gather_f32(pl, rk, i64, grid, s, p) : launch_contig_f32(pl, rk, i64, grid, s, p);
+        gather ? launch_gather_f32(pl, rk, i64, grid, s, p)
+               : (p.src_nt ? launch_contig_f32_nt : launch_contig_f32)(pl, rk, i64, grid, s, p);
         break;
       case OGN_F16:
-        gather ? launch_gather_f16(pl, rk, i64, grid, s, p) : launch_contig_f16(pl, rk, i64, grid, s, p);
+        gather ? launch_gather_f16(pl, rk, i64, grid, s, p)
+               : (p.src_nt ? launch_contig_f16_nt : launch_contig_f16)(pl, rk, i64, grid, s, p);
         break;
       case OGN_I8:
         launch_gather_i8(pl, rk, i64, grid, s, p);  // gather mode only (torch_sparse int8 SpMM)
         break;
       default:
-        gather ? launch_gather_bf16(pl, rk, i64, grid, s, p) : launch_contig_bf16(pl, rk, i64, grid, s, p);
+        gather ? launch_gather_bf16(pl, rk, i64, grid, s, p)
+               : (p.src_nt ? launch_contig_bf16_nt : launch_contig_bf16)(pl, rk, i64, grid, s, p);
         break;
     }
   }

@@ -178,3 +178,42 @@ def test_staged_and_direct_row_stores_agree(ogn, chunk, reduce, feat):
     for a, b in zip(staged, direct):
         assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a,
                            b.view(torch.int32) if b.dtype == torch.float32 else b)
+
+
+@pytest.mark.parametrize("op", ["sum", "max", "logsumexp", "scatter_max"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("feat", [1, 32, 33])
+def test_nontemporal_and_plain_source_loads_agree(ogn, oracle, chunk, op, dtype, feat):
+    # the library reads a contiguous source above 256 MiB with non-temporal
+    # loads (separate kernel instances) and a smaller one with plain loads;
+    # OGN_ENGINE_NT=1 / 0 forces either: same bits, and the oracle's values
+    lengths = _lengths(70 + feat)
+    rng = np.random.default_rng(80 + feat)
+    ptr_np = np.concatenate([[0], np.cumsum(lengths)])
+    indptr = torch.from_numpy(ptr_np).cuda()
+    src = _src(rng, int(lengths.sum()), feat, dtype, op in ("max", "scatter_max"))
+    dsrc = src.cuda()
+    index = torch.from_numpy(np.repeat(np.arange(lengths.size), lengths)).cuda()
+
+    def run():
+        if op == "logsumexp":
+            return (ogn.segment_logsumexp(dsrc, indptr),)
+        if op == "scatter_max":
+            return ogn.scatter_max(dsrc, index, 0, None, lengths.size)
+        res = getattr(ogn, f"segment_{op}_csr")(dsrc, indptr)
+        return res if isinstance(res, tuple) else (res,)
+
+    outs = {}
+    for mode in ("1", "0"):
+        os.environ["OGN_ENGINE_NT"] = mode
+        try:
+            outs[mode] = [t.cpu() for t in run()]
+        finally:
+            os.environ.pop("OGN_ENGINE_NT", None)
+    for a, b in zip(outs["1"], outs["0"]):
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b)
+    if op == "max":
+        gold, garg = oracle.segment_csr(src, ptr_np, "max")
+        assert_exact(outs["1"][0], cast_like(gold, dtype), "nt max values")
+        assert_exact(outs["1"][1], garg, "nt max arg")
