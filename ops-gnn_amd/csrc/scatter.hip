@@ -417,6 +417,31 @@ __global__ __launch_bounds__(256) void group_bwd_messages_kernel(const void* sav
   }
 }
 
+// The same in 16-byte packets (n a multiple of the packet, aligned buffers).
+template <int DT>
+__global__ __launch_bounds__(256) void group_bwd_messages_vec_kernel(const void* saved, const void* grad, int64_t n,
+                                                                     int mode, float* __restrict__ msg) {
+  using E = Elem<DT>;
+  using S_t = typename E::S;
+  constexpr int NE = E::VEC;
+  const S_t* __restrict__ sv = static_cast<const S_t*>(saved);
+  const S_t* __restrict__ gr = static_cast<const S_t*>(grad);
+  const int64_t packets = n / NE;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < packets; p += stride) {
+    const int64_t i0 = p * NE;
+    float g[NE];
+    E::unpack(load16(gr + i0), g);
+    if (mode == 0) {
+      float y[NE];
+      E::unpack(load16(sv + i0), y);
+#pragma unroll
+      for (int i = 0; i < NE; ++i) g[i] = y[i] * g[i];
+    }
+    store_floats<NE>(msg, OGN_F32, i0, g);
+  }
+}
+
 __global__ __launch_bounds__(256) void group_bwd_apply_kernel(GroupBwdArgs a) {
   const int64_t total = a.before * a.len * a.after;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -690,7 +715,16 @@ int ogn_group_bwd_messages(const void* saved, const void* grad, int dtype, int64
   if (!grad || !msg || (mode == 0 && !saved)) return fail(OGN_EINVAL, "ogn_group_bwd_messages: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   TimedLaunch t("group_bwd_messages", st);
-  hipLaunchKernelGGL(group_bwd_messages_kernel, dim3(grid_for(n)), dim3(256), 0, st, saved, grad, dtype, n, mode, msg);
+  const int ne = 16 / dtype_size(dtype);
+  auto al = [](const void* q) { return (uintptr_t)q % 16 == 0; };
+  if (n % ne == 0 && al(grad) && al(msg) && (mode == 1 || al(saved))) {
+    const dim3 g(grid_for(n / ne));
+    if (dtype == OGN_F32) hipLaunchKernelGGL(group_bwd_messages_vec_kernel<OGN_F32>, g, dim3(256), 0, st, saved, grad, n, mode, msg);
+    else if (dtype == OGN_F16) hipLaunchKernelGGL(group_bwd_messages_vec_kernel<OGN_F16>, g, dim3(256), 0, st, saved, grad, n, mode, msg);
+    else hipLaunchKernelGGL(group_bwd_messages_vec_kernel<OGN_BF16>, g, dim3(256), 0, st, saved, grad, n, mode, msg);
+  } else {
+    hipLaunchKernelGGL(group_bwd_messages_kernel, dim3(grid_for(n)), dim3(256), 0, st, saved, grad, dtype, n, mode, msg);
+  }
   return check_launch("ogn_group_bwd_messages");
 }
 
