@@ -158,6 +158,9 @@ int run(const Plan& pl, Params& p, int in_dtype, int index_dtype, bool gather, i
   bool nt = src_bytes > 256.0 * 1024 * 1024;
   if (const char* env = std::getenv("OGN_ENGINE_NT")) nt = std::atoi(env) != 0;
   p.src_nt = !gather && in_dtype != OGN_I8 && nt && variant_of(rk, false, p) != V_GENERIC;
+  // extremum positions of outputs larger than that cache: non-temporal
+  const double out_bytes = (double)batch * (double)p.m * (double)p.k * (double)(dtype_size(p.out_dt) + 8);
+  p.out_nt = rk == RK_MINMAX && out_bytes > 256.0 * 1024 * 1024;
   const KeptKey kl{workspace, p.ptr, {0, p.ptr_bstride, ptr_batches, p.m, p.nnz_bound, pl.chunk, pl.nchunks,
                                        index_dtype}, {}};
   if (!(layout & LAYOUT_REUSE) || !kept_layout_match(kl)) {
